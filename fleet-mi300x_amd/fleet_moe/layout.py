@@ -1,0 +1,173 @@
+"""The reference's packed-weight layout and manifest, for the MoE tensors.
+
+Layout contract (src/host/pack_weights.py:41-54, 71-83, 125-146): one flat
+blob of bf16 values; every tensor starts on a 256-byte boundary;
+`L{i}.router` is [n_routed][hidden]; `L{i}.experts` is n_routed contiguous
+blocks of `expert_stride` = 3 * hidden * moe_inter elements, each block the
+gate/up rows interleaved [g0, u0, g1, u1, ...] followed by down
+[hidden][moe_inter]; `L{i}.shared` is the interleaved gate/up of the merged
+shared expert followed by its down [hidden][n_shared * moe_inter];
+`L{i}.norm_post` is the post-attention RMSNorm weight. The manifest is text,
+`scalar <name> <repr>` lines then `tensor <name> <byte offset> <bytes>` lines
+(pack_weights.py:86-93), which is the grammar the reference launcher parses
+(src/host/fleet_launch.hip:154-170).
+
+This module only computes offsets and packs NumPy arrays; moving the blob to
+the GPU is the caller's business (fleet_moe.ops).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+ALIGN = 256
+
+
+@dataclass(frozen=True)
+class MoeDims:
+    """MoE shape and scalars (the manifest's scalars, pack_weights.py:153-184)."""
+    hidden: int = 2048
+    moe_inter: int = 1408
+    n_routed: int = 64
+    n_shared: int = 2
+    top_k: int = 6
+    routed_scaling: float = 1.0
+    rms_eps: float = 1e-6
+
+    @property
+    def shared_inter(self) -> int:
+        return self.n_shared * self.moe_inter
+
+    @property
+    def expert_stride(self) -> int:
+        """Elements per routed expert block: gate/up (2*I*H) + down (H*I)."""
+        return 3 * self.hidden * self.moe_inter
+
+    @property
+    def shared_elems(self) -> int:
+        return 3 * self.hidden * self.shared_inter
+
+
+DSV2_LITE = MoeDims()
+
+
+@dataclass
+class TensorEntry:
+    name: str
+    offset: int      # bytes from the blob base
+    nbytes: int
+    shape: tuple
+
+
+@dataclass
+class Layout:
+    """Offsets of tensors in one blob, 256-byte aligned, in insertion order."""
+    tensors: dict = field(default_factory=dict)
+    scalars: dict = field(default_factory=dict)
+    pos: int = 0
+
+    def add(self, name: str, shape, itemsize: int = 2) -> TensorEntry:
+        if name in self.tensors:
+            raise ValueError(f"duplicate tensor {name}")
+        self.pos += (-self.pos) % ALIGN
+        n = int(np.prod(shape)) * itemsize
+        e = TensorEntry(name, self.pos, n, tuple(int(s) for s in shape))
+        self.tensors[name] = e
+        self.pos += n
+        return e
+
+    @property
+    def nbytes(self) -> int:
+        return self.pos
+
+    def manifest(self) -> str:
+        """Manifest text in the reference's grammar (pack_weights.py:86-93)."""
+        lines = []
+        for k, v in self.scalars.items():
+            if isinstance(v, (int, float)) and not isinstance(v, bool):
+                lines.append(f"scalar {k} {v!r}\n")
+        for name, t in self.tensors.items():
+            lines.append(f"tensor {name} {t.offset} {t.nbytes}\n")
+        return "".join(lines)
+
+
+def parse_manifest(text: str):
+    """Parse `scalar`/`tensor` lines (grammar of fleet_launch.hip:154-170).
+
+    Returns (scalars: dict name -> int|float, tensors: dict name -> (offset,
+    bytes)). Raises ValueError on a malformed line.
+    """
+    scalars, tensors = {}, {}
+    for ln, line in enumerate(text.splitlines(), 1):
+        parts = line.split()
+        if not parts:
+            continue
+        if parts[0] == "scalar" and len(parts) == 3:
+            v = parts[2]
+            try:
+                scalars[parts[1]] = int(v)
+            except ValueError:
+                scalars[parts[1]] = float(v)
+        elif parts[0] == "tensor" and len(parts) == 4:
+            tensors[parts[1]] = (int(parts[2]), int(parts[3]))
+        else:
+            raise ValueError(f"manifest line {ln}: {line!r}")
+    return scalars, tensors
+
+
+def moe_layout(dims: MoeDims = DSV2_LITE, layers=(1,), with_norm: bool = True) -> Layout:
+    """Layout of the MoE tensors of `layers` (pack_weights.py:113-142 order:
+    norm_post first, then router, experts, shared)."""
+    lay = Layout()
+    H = dims.hidden
+    for i in layers:
+        if with_norm:
+            lay.add(f"L{i}.norm_post", (H,))
+        lay.add(f"L{i}.router", (dims.n_routed, H))
+        lay.add(f"L{i}.experts", (dims.n_routed * dims.expert_stride,))
+        lay.add(f"L{i}.shared", (dims.shared_elems,))
+    lay.scalars.update({
+        "bytes": lay.nbytes, "expert_stride": dims.expert_stride, "hidden": H,
+        "moe_inter": dims.moe_inter, "n_routed": dims.n_routed, "n_shared": dims.n_shared,
+        "top_k": dims.top_k, "rms_eps": dims.rms_eps, "routed_scaling": float(dims.routed_scaling),
+    })
+    return lay
+
+
+def dims_from_scalars(s: dict) -> MoeDims:
+    """MoeDims from manifest scalars."""
+    return MoeDims(hidden=int(s["hidden"]), moe_inter=int(s["moe_inter"]),
+                   n_routed=int(s["n_routed"]), n_shared=int(s["n_shared"]),
+                   top_k=int(s["top_k"]), routed_scaling=float(s.get("routed_scaling", 1.0)),
+                   rms_eps=float(s.get("rms_eps", 1e-6)))
+
+
+# ---------------------------------------------------------------- packing
+
+def interleave_gate_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """Rows [g0, u0, g1, u1, ...] (pack_weights.py:71-83)."""
+    if gate.shape != up.shape:
+        raise ValueError(f"gate {gate.shape} vs up {up.shape}")
+    out = np.empty((2 * gate.shape[0], gate.shape[1]), dtype=gate.dtype)
+    out[0::2] = gate
+    out[1::2] = up
+    return out
+
+
+def pack_expert(gate: np.ndarray, up: np.ndarray, down: np.ndarray) -> np.ndarray:
+    """One expert block: interleaved gate/up then down, flattened (uint16)."""
+    return np.concatenate([interleave_gate_up(gate, up).reshape(-1), down.reshape(-1)])
+
+
+def write_blob(blob: np.ndarray, entry: TensorEntry, arr: np.ndarray) -> None:
+    """Copy bf16 bits `arr` into the uint8 blob at entry's offset."""
+    a = np.ascontiguousarray(arr, dtype=np.uint16).reshape(-1)
+    if a.nbytes != entry.nbytes:
+        raise ValueError(f"{entry.name}: {a.nbytes} bytes, layout has {entry.nbytes}")
+    blob[entry.offset: entry.offset + a.nbytes] = a.view(np.uint8)
+
+
+def view_u16(blob: np.ndarray, entry: TensorEntry) -> np.ndarray:
+    """uint16 view of one tensor of a uint8 blob."""
+    return blob[entry.offset: entry.offset + entry.nbytes].view(np.uint16)

@@ -1,0 +1,137 @@
+/*
+ * fleet_moe.h -- C ABI of the MI355X (gfx950) batch-1 MoE decode path for
+ * DeepSeek-V2-Lite: router + greedy top-k, routed SwiGLU experts, the fused
+ * shared expert, the weighted combine, and the multi-token grouped product.
+ *
+ * Conventions (match the reference launcher's, src/host/fleet_launch.hip:55-63,
+ * 612-644, and its task-body ABI, src/kernels/fleet_kernel.hip:1057-1078):
+ *   - every entry point returns 0 on success, a hipError_t value when a HIP
+ *     call fails, or a FLEET_MOE_ERR_* code (>= 10000) for a rejected argument;
+ *   - nothing here allocates: the caller owns every buffer (weights, inputs,
+ *     outputs, workspace) as device memory, and passes plain device pointers;
+ *   - work is enqueued on `stream` and is asynchronous; inputs are read-only;
+ *   - a workspace must be zero-filled once before its first use and may then
+ *     be reused by any number of calls that are ordered on one stream; two
+ *     calls that overlap in time must not share a workspace;
+ *   - weights use the reference's packed layout (src/host/pack_weights.py:
+ *     41-54, 71-83, 125-146): bf16 bit patterns (uint16_t), experts as
+ *     n_routed blocks of `expert_stride` elements [gate/up interleaved
+ *     (2*I rows of H) | down (H rows of I)], the merged shared expert as
+ *     [gate/up interleaved (2*SI rows of H) | down (H rows of SI)], SI =
+ *     n_shared * I. Tensor bases must be 16-byte aligned (the packer aligns
+ *     every tensor to 256 bytes).
+ * The kernels are built for the DeepSeek-V2-Lite shape (hidden 2048,
+ * moe_inter 1408, 64 routed experts, top-6, 2 shared experts); other shapes
+ * are rejected with FLEET_MOE_ERR_DIMS.
+ */
+#ifndef FLEET_MOE_H
+#define FLEET_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLEET_MOE_ERR_DIMS 10001      /* shape other than the supported one  */
+#define FLEET_MOE_ERR_ARG 10002       /* null or misaligned pointer, bad count */
+#define FLEET_MOE_ERR_WORKSPACE 10003 /* workspace smaller than required      */
+#define FLEET_MOE_ERR_DEVICE 10004    /* device is not gfx950 / too few CUs   */
+
+/* Model scalars, the MoE subset of ModelDims (src/runtime/fleet_types.h:33-39)
+ * and of the packed manifest's scalars (src/host/pack_weights.py:153-184). */
+typedef struct fleet_moe_dims {
+    int32_t hidden;        /* 2048 */
+    int32_t moe_inter;     /* 1408 */
+    int32_t n_routed;      /* 64   */
+    int32_t n_shared;      /* 2: the shared expert has n_shared*moe_inter rows */
+    int32_t top_k;         /* 6    */
+    float routed_scaling;  /* 1.0  */
+    float rms_eps;         /* 1e-6 */
+} fleet_moe_dims;
+
+/* One MoE layer's weights: the per-layer pointer tables of Weights
+ * (src/runtime/fleet_types.h:44-59: layer_norm_post, layer_router,
+ * layer_experts, layer_shared, expert_stride). */
+typedef struct fleet_moe_layer {
+    const uint16_t* norm;     /* post-attention RMSNorm weight bf16[hidden]; NULL = unit */
+    const uint16_t* router;   /* bf16[n_routed][hidden] ("L{i}.router") */
+    const uint16_t* experts;  /* n_routed blocks ("L{i}.experts") */
+    int64_t expert_stride;    /* elements between experts: 3*hidden*moe_inter */
+    const uint16_t* shared;   /* merged shared expert block ("L{i}.shared") */
+} fleet_moe_layer;
+
+/* Router logits and greedy top-k for n_tokens rows of x_norm.
+ * Replaces the router GEMV of task_norm_router (src/kernels/fleet_kernel.hip:
+ * 433-435) and select_experts_from (:469-494); semantics of
+ * src/host/reference_decode.py:271-278 and HF MoEGate.forward
+ * (reference/modeling_deepseek.py:420-467):
+ *   logits = W_router . x_norm (fp32; evaluated exactly and rounded once),
+ *   p = softmax(logits + logit_bias), ids = the top_k largest p in decreasing
+ *   order, ties to the lowest index, weights = p[ids] * routed_scaling.
+ * x_norm: fp32[n_tokens][hidden] (bf16-valued); logit_bias: fp32[n_routed]
+ * or NULL; logits: fp32[n_tokens][n_routed] or NULL; ids: int32[n_tokens]
+ * [top_k]; weights: fp32[n_tokens][top_k]. 1 <= n_tokens <= 65535. */
+int fleet_moe_router_topk(const uint16_t* router, const float* x_norm, int32_t n_tokens,
+                          const float* logit_bias, float* logits, int32_t* ids,
+                          float* weights, const fleet_moe_dims* dims, hipStream_t stream);
+
+/* Workspace bytes fleet_moe_layer_decode needs. */
+size_t fleet_moe_layer_workspace_bytes(const fleet_moe_dims* dims);
+
+/* One batch-1 MoE layer: x_out = bf16(x + moe(rms_norm(x))).
+ * Replaces, for one token, the NORM_ROUTER (kind 4), EXPERT_GATE_UP (5) and
+ * EXPERT_DOWN (6) task bodies and the expert-partial fold (src/kernels/
+ * fleet_kernel.hip:398-456, 469-500, 826-889, 146-201; src/kernels/expert.h:
+ * 45-116); semantics of src/host/reference_decode.py:294-302 (rms_norm, moe,
+ * residual add) with the selection rule above.
+ * x: fp32[hidden]; x_out: fp32[hidden] (may equal x); moe_out: bf16[hidden]
+ * (the MoE output before the residual add) or NULL; ids: int32[top_k] or
+ * NULL; weights: fp32[top_k] or NULL. Launches one cooperative kernel over
+ * every CU of the device. */
+int fleet_moe_layer_decode(const fleet_moe_layer* layer, const float* x, float* x_out,
+                           uint16_t* moe_out, int32_t* ids, float* weights,
+                           void* workspace, size_t workspace_bytes,
+                           const fleet_moe_dims* dims, hipStream_t stream);
+
+/* Workspace bytes fleet_moe_grouped needs for up to max_tokens tokens. */
+size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, int32_t max_tokens);
+
+/* Multi-token grouped-expert product for one layer (no reference kernel; HF
+ * DeepseekV2MoE.forward + moe_infer, reference/modeling_deepseek.py:568-664):
+ * tokens are permuted by expert, every selected expert runs its SwiGLU over
+ * its token rows (bf16 MFMA where an expert holds >= 16 tokens, GEMV below),
+ * and out[t] = bf16(bf16(sum_k bf16(w[t][k] * E_{ids[t][k]}(x[t]))) +
+ * shared(x[t])), the per-token combine of src/host/reference_decode.py:
+ * 280-287, so grouped(T) equals T batch-1 MoE outputs.
+ * x_norm: bf16[n_tokens][hidden]; ids: int32[n_tokens][top_k] (each in
+ * [0, n_routed), distinct per token); weights: fp32[n_tokens][top_k];
+ * out: bf16[n_tokens][hidden]. 1 <= n_tokens <= max_tokens of the workspace. */
+int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens, const int32_t* ids,
+                      const float* weights, const uint16_t* x_norm, uint16_t* out,
+                      void* workspace, size_t workspace_bytes, const fleet_moe_dims* dims,
+                      hipStream_t stream);
+
+/* Copies the workspace's sticky status word to *status (0 = healthy; a
+ * nonzero value names a bounded wait that expired, see FLEET_MOE_ABORT_*),
+ * synchronising `stream`. The reference's equivalent is the sticky rt.abort
+ * word (src/runtime/fleet_runtime.h:194-198, 287-293). */
+int fleet_moe_workspace_status(const void* workspace, uint32_t* status, hipStream_t stream);
+
+#define FLEET_MOE_ABORT_ROUTER_WAIT 0x1u  /* router logits never published  */
+#define FLEET_MOE_ABORT_UNIT_WAIT 0x2u    /* an expert unit never completed */
+#define FLEET_MOE_ABORT_GROUP_WAIT 0x4u   /* grouped step phase never completed */
+
+/* Human-readable text for a return code of this library. */
+const char* fleet_moe_error_string(int code);
+
+/* ABI version of this header (major * 100 + minor). */
+int fleet_moe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLEET_MOE_H */

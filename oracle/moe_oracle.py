@@ -1,0 +1,408 @@
+"""CPU oracle for the batch-1 DeepSeek-V2-Lite MoE decode path.
+
+TEST INFRASTRUCTURE ONLY. This module is the checker the HIP path is compared
+against; it is imported by `tests/`, by `__graft_entry__.smoke()` and by the
+`cpu_baseline` leg of `bench.py`, and by nothing the product ships. The
+product path (the `fleet_moe` package and `libfleet_moe.so`) never calls it.
+
+It restates, in plain NumPy, the task semantics of the reference's
+`src/host/reference_decode.py` (cited per function below) together with the
+selection rule of the reference kernel (`src/kernels/fleet_kernel.hip`) and
+the multi-token semantics of HF's `DeepseekV2MoE.moe_infer`
+(`reference/modeling_deepseek.py:591-664`). All citations are relative to the
+reference repository root.
+
+Arithmetic choices, each one the exact value the reference's fp32 arithmetic
+approximates (the reference leaves the rounding of these reductions to
+OpenBLAS / numpy and is therefore only defined up to a few fp32 ulps):
+
+* the RMSNorm mean of squares, the router dot products and the softmax are
+  evaluated in fp64 and rounded once to fp32. Every router product is a
+  product of two bf16 values, so these sums are exact to ~1e-16 relative and
+  independent of summation order, which makes the routed expert ids a
+  deterministic function of the inputs (the GPU path computes them the same
+  way, so ids compare bit-exactly);
+* SiLU is evaluated in fp64 and rounded to fp32 before the bf16 rounding;
+* the expert GEMVs accumulate in fp32 (NumPy/OpenBLAS order), exactly as
+  `reference_decode.mlp_unit` does; the GPU accumulates in fp32 in its own
+  order, so expert outputs are compared at bf16 tolerance (rel 1e-2).
+
+Parity status of each function (how it is pinned) is listed in
+`tests/test_oracle.py`; every function here is pinned by at least one check
+that does not retype its formula.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+# DeepSeek-V2-Lite shapes (reference/dsv2lite_config.json).
+HIDDEN = 2048
+MOE_INTER = 1408
+N_ROUTED = 64
+N_SHARED = 2
+TOP_K = 6
+RMS_EPS = 1e-6
+ROUTED_SCALING = 1.0
+
+
+# ---------------------------------------------------------------- bf16
+
+def bf16_round(x) -> np.ndarray:
+    """Round fp32 to the nearest bf16, ties to even, returned as fp32.
+
+    Restates reference_decode.py:37-48 (the same add-0x7FFF-plus-odd-bit RNE
+    formula on the fp32 bit pattern). Finite inputs only.
+    """
+    x = np.array(x, dtype=np.float32)
+    u = x.view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return r.astype(np.uint32).view(np.float32)
+
+
+def bf16_bits(x) -> np.ndarray:
+    """bf16 bit patterns (uint16) of the RNE rounding of fp32 `x`."""
+    return (bf16_round(x).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    """Widen bf16 bit patterns (uint16) to fp32 exactly."""
+    b = np.asarray(bits, dtype=np.uint16)
+    return (b.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+# ---------------------------------------------------------------- a1 RMSNorm
+
+def rms_norm(x, gamma=None, eps: float = RMS_EPS) -> np.ndarray:
+    """DeepseekV2RMSNorm with HF's two bf16 roundings.
+
+    reference_decode.py:51-65 (bf16=True) and fleet_kernel.hip:83-96:
+    y = bf16(bf16(x * (1 / sqrt(mean(x^2) + eps))) * gamma).
+    The mean of squares is the fp64 sum rounded once to fp32; `1/sqrt` are
+    single fp32 operations (correctly rounded, as NumPy computes them).
+    `gamma=None` is the unit weight. Works on [..., H].
+    """
+    x32 = np.asarray(x, dtype=np.float32)
+    h = x32.shape[-1]
+    ssq = np.sum(x32.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    var = (ssq / h).astype(np.float32)
+    inv = np.float32(1.0) / np.sqrt(var + np.float32(eps))
+    y = bf16_round(x32 * inv)
+    g = np.float32(1.0) if gamma is None else np.asarray(gamma, dtype=np.float32)
+    return bf16_round(y * g)
+
+
+# ---------------------------------------------------------------- a2 router
+
+def router_logits(w_router, x_n) -> np.ndarray:
+    """fp32 router logits = W_g @ x_n.
+
+    reference_decode.py:271 (`w.gate_weight @ x_n`, fp32) and HF
+    modeling_deepseek.py:424-426 (F.linear in fp32). Evaluated in fp64 and
+    rounded once to fp32 (see module docstring). Accepts x_n of shape [H] or
+    [T, H]; returns [E] or [T, E].
+    """
+    w64 = np.asarray(w_router, dtype=np.float32).astype(np.float64)
+    x64 = np.asarray(x_n, dtype=np.float32).astype(np.float64)
+    return (x64 @ w64.T).astype(np.float32)
+
+
+# ---------------------------------------------------------------- a3 top-k
+
+def softmax(logits) -> np.ndarray:
+    """Softmax over the last axis: reference_decode.py:72-75, in fp64 then fp32."""
+    l64 = np.asarray(logits, dtype=np.float32).astype(np.float64)
+    m = np.max(l64, axis=-1, keepdims=True)
+    e = np.exp(l64 - m)
+    return (e / np.sum(e, axis=-1, keepdims=True)).astype(np.float32)
+
+
+def topk_lowest_index(scores, k: int):
+    """Greedy top-k with ties to the lowest index, in selection order.
+
+    The reference kernel's rule (fleet_kernel.hip:469-494: k passes of an
+    argmax in which an equal score with a smaller index wins); the NumPy
+    reference's `np.argpartition` (reference_decode.py:273) selects the same
+    set but leaves tie order unspecified, and HF's `torch.topk(sorted=False)`
+    (modeling_deepseek.py:436-438) likewise. Returns (ids int32[..., k],
+    values fp32[..., k]) ordered by decreasing score.
+    """
+    s = np.asarray(scores, dtype=np.float32)
+    # lexsort sorts by the last key first: primary -score, secondary index.
+    idx = np.arange(s.shape[-1])
+    if s.ndim == 1:
+        order = np.lexsort((idx, -s))[:k]
+        return order.astype(np.int32), s[order]
+    ids = np.stack([np.lexsort((idx, -row))[:k] for row in s]).astype(np.int32)
+    return ids, np.take_along_axis(s, ids, axis=-1)
+
+
+def route(w_router, x_n, top_k: int = TOP_K, routed_scaling: float = ROUTED_SCALING,
+          logit_bias=None):
+    """Router + softmax + greedy top-k, unnormalised weights x scaling.
+
+    reference_decode.py:271-278 with norm_topk_prob=False; `logit_bias`
+    (optional fp32 [E]) is added to the logits before the softmax, which is
+    how the skewed-load benchmark of the grouped step biases routing.
+    Returns (logits, ids, weights).
+    """
+    logits = router_logits(w_router, x_n)
+    z = logits if logit_bias is None else (logits + np.asarray(logit_bias, np.float32))
+    p = softmax(z)
+    ids, pv = topk_lowest_index(p, top_k)
+    return logits, ids, (pv * np.float32(routed_scaling)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- a5/a6 SwiGLU
+
+def silu(x) -> np.ndarray:
+    """x / (1 + exp(-x)) (reference_decode.py:68-69), fp64 then fp32."""
+    x64 = np.asarray(x, dtype=np.float32).astype(np.float64)
+    return (x64 / (1.0 + np.exp(-x64))).astype(np.float32)
+
+
+def swiglu_h(gate, up, x_n) -> np.ndarray:
+    """h = bf16(bf16(silu(bf16(gate x))) * bf16(up x)), fp32 GEMVs.
+
+    reference_decode.py:263-264 and the epilogue of gemv.h:537-542.
+    gate/up: [I, H] fp32 (bf16-valued); x_n: [H] or [T, H].
+    """
+    g = bf16_round(np.asarray(x_n, np.float32) @ np.asarray(gate, np.float32).T)
+    u = bf16_round(np.asarray(x_n, np.float32) @ np.asarray(up, np.float32).T)
+    return bf16_round(bf16_round(silu(g)) * u)
+
+
+def down_proj(down, h) -> np.ndarray:
+    """bf16(down @ h), fp32 GEMV: reference_decode.py:265."""
+    return bf16_round(np.asarray(h, np.float32) @ np.asarray(down, np.float32).T)
+
+
+def mlp_unit(gate, up, down, x_n) -> np.ndarray:
+    """One SwiGLU expert with HF's bf16 roundings: reference_decode.py:259-265."""
+    return down_proj(down, swiglu_h(gate, up, x_n))
+
+
+# ---------------------------------------------------------------- a4 packed layout
+
+@dataclass
+class PackedLayer:
+    """One MoE layer in the reference's packed-weight layout.
+
+    pack_weights.py:125-142: `router` is [E][H] bf16; `experts` is E blocks of
+    `expert_stride` elements, each the gate/up rows interleaved
+    [g0, u0, g1, u1, ...] ([2I][H]) followed by down ([H][I]); `shared` is the
+    interleaved gate/up of the merged shared expert ([2*SI][H]) followed by its
+    down ([H][SI]), SI = n_shared * I. Arrays hold bf16 bit patterns (uint16).
+    `norm` is the post-attention RMSNorm weight (bf16 bits) or None for unit.
+    """
+    router: np.ndarray
+    experts: np.ndarray
+    shared: np.ndarray
+    expert_stride: int
+    hidden: int = HIDDEN
+    moe_inter: int = MOE_INTER
+    n_shared: int = N_SHARED
+    norm: np.ndarray | None = None
+    cache: dict = field(default_factory=dict, repr=False)
+
+    @property
+    def shared_inter(self) -> int:
+        return self.n_shared * self.moe_inter
+
+    def router_f32(self) -> np.ndarray:
+        return bf16_to_f32(self.router).reshape(-1, self.hidden)
+
+    def gamma_f32(self):
+        return None if self.norm is None else bf16_to_f32(self.norm)
+
+    def expert_f32(self, e: int):
+        """(gate [I,H], up [I,H], down [H,I]) of routed expert e, fp32.
+
+        Addressing as expert.h:52-59: base = experts + e * stride,
+        down = base + 2 * I * H.
+        """
+        if int(e) in self.cache:
+            return self.cache[int(e)]
+        H, I = self.hidden, self.moe_inter
+        base = int(e) * self.expert_stride
+        gu = bf16_to_f32(self.experts[base: base + 2 * I * H]).reshape(2 * I, H)
+        dn = bf16_to_f32(self.experts[base + 2 * I * H: base + 3 * I * H]).reshape(H, I)
+        return np.ascontiguousarray(gu[0::2]), np.ascontiguousarray(gu[1::2]), dn
+
+    def shared_f32(self):
+        """(gate [SI,H], up [SI,H], down [H,SI]) of the merged shared expert."""
+        if "shared" in self.cache:
+            return self.cache["shared"]
+        H, SI = self.hidden, self.shared_inter
+        gu = bf16_to_f32(self.shared[: 2 * SI * H]).reshape(2 * SI, H)
+        dn = bf16_to_f32(self.shared[2 * SI * H: 3 * SI * H]).reshape(H, SI)
+        return np.ascontiguousarray(gu[0::2]), np.ascontiguousarray(gu[1::2]), dn
+
+    def widen(self, experts=None) -> None:
+        """Pre-widen experts (all if None) and the shared expert to fp32 and
+        keep them, so repeated oracle calls skip the bf16 -> fp32 conversion
+        (the reference's LayerWeights hold fp32 arrays, reference_decode.py:
+        139-163)."""
+        n = self.experts.size // self.expert_stride
+        for e in (range(n) if experts is None else experts):
+            if int(e) not in self.cache:
+                self.cache[int(e)] = self.expert_f32(int(e))
+        if "shared" not in self.cache:
+            self.cache["shared"] = self.shared_f32()
+
+
+def resolve_unit(layer: PackedLayer, slot: int, ids, weights):
+    """Map a descriptor routing slot to (gate_up, down, down_ld, weight, rows).
+
+    Restates expert.h:45-71 on flat uint16 arrays: slot k >= 0 is routed
+    expert ids[k] (base + id * stride, down after the 2*I*H gate/up block,
+    ld = I, weight = weights[k]); slot -1/-2 is half h of the shared expert
+    (gate/up rows [h*I, (h+1)*I) at element offset h*2*I*H, down columns
+    [h*I, (h+1)*I) of every row at offset 2*SI*H + h*I, ld = SI, weight 1).
+    Returns flat views plus the row count, like the device pointers.
+    """
+    H, I, SI = layer.hidden, layer.moe_inter, layer.shared_inter
+    if slot >= 0:
+        base = int(ids[slot]) * layer.expert_stride
+        gate_up = layer.experts[base: base + 2 * I * H]
+        down = layer.experts[base + 2 * I * H: base + layer.expert_stride]
+        return gate_up, down, I, float(weights[slot]), I
+    half = -slot - 1
+    rows = SI // 2
+    gate_up = layer.shared[half * 2 * rows * H: (half + 1) * 2 * rows * H]
+    down = layer.shared[2 * SI * H + half * rows:]
+    return gate_up, down, SI, 1.0, rows
+
+
+def unit_forward(gate_up, down, ld: int, weight: float, rows: int, x_n, hidden: int):
+    """One unit of the 8-unit split: bf16(weight * bf16(down_n . h)) per row n,
+    the unit arithmetic of gemv.h (gate_up epilogue :537-542, EPI_BF16 :244)."""
+    gu = bf16_to_f32(gate_up).reshape(2 * rows, hidden)
+    h = swiglu_h(gu[0::2], gu[1::2], x_n)
+    d = bf16_to_f32(np.asarray(down)[: (hidden - 1) * ld + rows])
+    idx = np.arange(hidden)[:, None] * ld + np.arange(rows)[None, :]
+    return bf16_round(np.float32(weight) * down_proj(d[idx], h))
+
+
+# ---------------------------------------------------------------- a7 combine
+
+def combine(routed_terms, shared_out) -> np.ndarray:
+    """moe = bf16(bf16(sum_k t_k) + shared), t_k = bf16(w_k * E_k(x_n)).
+
+    reference_decode.py:280-287; the fp32 sum runs over k in selection order
+    (the reference runs it in argpartition order; the terms are bf16 values
+    whose fp32 sum is exact unless their exponents differ by more than 16).
+    """
+    y = np.zeros_like(np.asarray(shared_out, np.float32))
+    for t in routed_terms:
+        y = (y + np.asarray(t, np.float32)).astype(np.float32)
+    return bf16_round(bf16_round(y) + np.asarray(shared_out, np.float32))
+
+
+def moe(layer: PackedLayer, x_n, top_k: int = TOP_K,
+        routed_scaling: float = ROUTED_SCALING, logit_bias=None) -> dict:
+    """Router + top-k routed experts + shared expert for one token.
+
+    reference_decode.py:268-287 (`moe`) with the lowest-index tie rule.
+    Returns dict(logits, ids, weights, out) with out the bf16-valued fp32 [H].
+    """
+    x_n = np.asarray(x_n, np.float32)
+    logits, ids, ws = route(layer.router_f32(), x_n, top_k, routed_scaling, logit_bias)
+    terms = []
+    for k, e in enumerate(ids):
+        g, u, d = layer.expert_f32(int(e))
+        terms.append(bf16_round(ws[k] * mlp_unit(g, u, d, x_n)))
+    sg, su, sd = layer.shared_f32()
+    out = combine(terms, mlp_unit(sg, su, sd, x_n))
+    return {"logits": logits, "ids": ids, "weights": ws, "out": out}
+
+
+def moe_layer(layer: PackedLayer, x, top_k: int = TOP_K,
+              routed_scaling: float = ROUTED_SCALING, eps: float = RMS_EPS) -> dict:
+    """The MoE half of a decoder layer: x' = bf16(x + moe(rms_norm(x))).
+
+    reference_decode.py:301-302 (post-attention norm, MoE, bf16 residual add).
+    Returns dict(x_n, logits, ids, weights, out, x_out).
+    """
+    x = np.asarray(x, np.float32)
+    x_n = rms_norm(x, layer.gamma_f32(), eps)
+    r = moe(layer, x_n, top_k, routed_scaling)
+    r["x_n"] = x_n
+    r["x_out"] = bf16_round(x + r["out"])
+    return r
+
+
+# ---------------------------------------------------------------- a8 grouped
+
+def moe_grouped(layer: PackedLayer, x_n, ids, weights, combine_rule: str = "decode") -> dict:
+    """Multi-token MoE product with HF `moe_infer` data movement.
+
+    modeling_deepseek.py:591-664: count tokens per expert (cnts.scatter_),
+    argsort the flat (token, slot) ids, gather sorted_tokens = x[idxs // k],
+    run each expert's SwiGLU on its contiguous rows, scatter back
+    new_x[idxs] = outs, then combine per token; shared expert on every token
+    (modeling_deepseek.py:586-587).
+
+    combine_rule "decode": reference_decode.py:283-287 per token (bf16 of each
+    weighted expert output, fp32 sum in slot order, bf16, + bf16 shared) --
+    the rule the batch-1 path uses, so grouped(T) equals T batch-1 calls.
+    combine_rule "hf": moe_infer's `.type(fp32).mul_(w).sum(1).type(bf16)`
+    then the bf16 add of the shared output.
+    x_n: [T, H] bf16-valued; ids int [T, k]; weights fp32 [T, k].
+    Returns dict(out [T,H], tokens_per_expert [E], order (argsort) [T*k]).
+    """
+    x_n = np.asarray(x_n, np.float32)
+    ids = np.asarray(ids, np.int64)
+    ws = np.asarray(weights, np.float32)
+    T, k = ids.shape
+    E = layer.experts.size // layer.expert_stride
+    cnts = np.zeros((T, E), np.int64)
+    np.put_along_axis(cnts, ids, 1, axis=1)
+    tokens_per_expert = cnts.sum(axis=0)
+    flat = ids.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    sorted_tokens = x_n[order // k]
+    outs = np.empty((T * k, layer.hidden), np.float32)
+    start = 0
+    for e in range(E):
+        n = int(tokens_per_expert[e])
+        if n == 0:
+            continue
+        g, u, d = layer.expert_f32(e)
+        outs[start: start + n] = mlp_unit(g, u, d, sorted_tokens[start: start + n])
+        start += n
+    new_x = np.empty_like(outs)
+    new_x[order] = outs
+    per_slot = new_x.reshape(T, k, layer.hidden)
+    sg, su, sd = layer.shared_f32()
+    shared = mlp_unit(sg, su, sd, x_n)
+    if combine_rule == "decode":
+        out = np.stack([combine([bf16_round(ws[t, j] * per_slot[t, j]) for j in range(k)],
+                                shared[t]) for t in range(T)])
+    elif combine_rule == "hf":
+        y = np.zeros((T, layer.hidden), np.float32)
+        for j in range(k):
+            y = (y + per_slot[:, j] * ws[:, j: j + 1]).astype(np.float32)
+        out = bf16_round(bf16_round(y) + shared)
+    else:
+        raise ValueError(f"unknown combine_rule {combine_rule!r}")
+    return {"out": out, "tokens_per_expert": tokens_per_expert, "order": order}
+
+
+# ---------------------------------------------------------------- a9 byte model
+
+def moe_bytes(hidden: int = HIDDEN, moe_inter: int = MOE_INTER, top_k: int = TOP_K,
+              n_shared: int = N_SHARED, n_routed: int = N_ROUTED, distinct=None) -> dict:
+    """Algorithmic bytes of one MoE layer per token (bf16 weights).
+
+    model_analysis.py:92-99: each selected routed expert streams
+    3 * H * I * 2 bytes, the shared expert 3 * H * (n_shared * I) * 2, the
+    router E * H * 2. `distinct` overrides the routed count (grouped step).
+    """
+    per_expert = 3 * hidden * moe_inter * 2
+    shared = 3 * hidden * n_shared * moe_inter * 2
+    router = n_routed * hidden * 2
+    n = top_k if distinct is None else int(distinct)
+    return {"expert": per_expert, "shared": shared, "router": router,
+            "selected": n * per_expert + shared}

@@ -1,0 +1,103 @@
+"""The C-ABI library: it loads, exports every symbol include/fleet_moe.h
+declares, and rejects bad arguments before touching a device (CPU-only)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from fleet_moe import _lib
+from fleet_moe.layout import DSV2_LITE, MoeDims
+from fleet_moe.ops import c_dims
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fleet_moe.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(fleet_moe_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    decl = declared_functions()
+    assert decl, "no declarations parsed"
+    bound = {name for name, _, _ in _lib.SYMBOLS}
+    assert decl == bound, f"header vs binding: {sorted(decl ^ bound)}"
+    for name in decl:
+        assert getattr(lib, name) is not None
+
+
+def test_struct_layouts_match_header():
+    # fleet_moe_dims: 5 int32 + 2 float; fleet_moe_layer: 4 pointers + int64
+    assert ctypes.sizeof(_lib.FleetMoeDims) == 28
+    assert ctypes.sizeof(_lib.FleetMoeLayer) == 40
+    assert _lib.FleetMoeLayer.expert_stride.offset == 24
+
+
+def test_version_and_error_strings(lib):
+    assert lib.fleet_moe_abi_version() == 100
+    assert b"shape" in lib.fleet_moe_error_string(_lib.ERR_DIMS)
+    assert b"workspace" in lib.fleet_moe_error_string(_lib.ERR_WORKSPACE)
+    assert lib.fleet_moe_error_string(0) == b"success"
+
+
+def test_workspace_sizes(lib):
+    d = c_dims(DSV2_LITE)
+    n = lib.fleet_moe_layer_workspace_bytes(ctypes.byref(d))
+    assert n % 256 == 0 and 16_384 <= n <= 1 << 20
+    g64 = lib.fleet_moe_grouped_workspace_bytes(ctypes.byref(d), 64)
+    g16 = lib.fleet_moe_grouped_workspace_bytes(ctypes.byref(d), 16)
+    assert g64 > g16 > 0
+    assert lib.fleet_moe_grouped_workspace_bytes(ctypes.byref(d), 0) == 0
+    assert lib.fleet_moe_grouped_workspace_bytes(ctypes.byref(d), 100_000) == 0
+
+
+def test_bad_dims_rejected_without_device(lib):
+    bad = c_dims(MoeDims(hidden=4096))
+    layer = _lib.FleetMoeLayer(None, 16, 16, DSV2_LITE.expert_stride, 16)
+    rc = lib.fleet_moe_layer_decode(ctypes.byref(layer), 16, 16, None, None, None, 256, 1 << 20,
+                                    ctypes.byref(bad), None)
+    assert rc == _lib.ERR_DIMS
+    rc = lib.fleet_moe_router_topk(16, 16, 1, None, None, 16, 16, ctypes.byref(bad), None)
+    assert rc == _lib.ERR_DIMS
+    rc = lib.fleet_moe_grouped(ctypes.byref(layer), 4, 16, 16, 16, 16, 256, 1 << 24,
+                               ctypes.byref(bad), None)
+    assert rc == _lib.ERR_DIMS
+    topk = c_dims(MoeDims(top_k=8))
+    assert lib.fleet_moe_router_topk(16, 16, 1, None, None, 16, 16, ctypes.byref(topk), None) == _lib.ERR_DIMS
+
+
+def test_bad_pointers_rejected_without_device(lib):
+    d = c_dims(DSV2_LITE)
+    layer = _lib.FleetMoeLayer(None, 256, 256, DSV2_LITE.expert_stride, 256)
+    # null x
+    assert lib.fleet_moe_layer_decode(ctypes.byref(layer), None, 256, None, None, None, 256,
+                                      1 << 20, ctypes.byref(d), None) == _lib.ERR_ARG
+    # misaligned experts base
+    mis = _lib.FleetMoeLayer(None, 256, 258, DSV2_LITE.expert_stride, 256)
+    assert lib.fleet_moe_layer_decode(ctypes.byref(mis), 256, 256, None, None, None, 256,
+                                      1 << 20, ctypes.byref(d), None) == _lib.ERR_ARG
+    # stride smaller than one expert
+    short = _lib.FleetMoeLayer(None, 256, 256, DSV2_LITE.expert_stride - 8, 256)
+    assert lib.fleet_moe_layer_decode(ctypes.byref(short), 256, 256, None, None, None, 256,
+                                      1 << 20, ctypes.byref(d), None) == _lib.ERR_DIMS
+    # workspace too small
+    assert lib.fleet_moe_layer_decode(ctypes.byref(layer), 256, 256, None, None, None, 256,
+                                      64, ctypes.byref(d), None) == _lib.ERR_WORKSPACE
+    # token counts out of range
+    assert lib.fleet_moe_router_topk(256, 256, 0, None, None, 256, 256, ctypes.byref(d), None) == _lib.ERR_ARG
+    assert lib.fleet_moe_grouped(ctypes.byref(layer), 0, 256, 256, 256, 256, 256, 1 << 26,
+                                 ctypes.byref(d), None) == _lib.ERR_ARG
+    assert lib.fleet_moe_grouped(ctypes.byref(layer), 300, 256, 256, 256, 256, 256, 1 << 26,
+                                 ctypes.byref(d), None) == _lib.ERR_ARG
+    small = lib.fleet_moe_grouped_workspace_bytes(ctypes.byref(d), 4)
+    assert lib.fleet_moe_grouped(ctypes.byref(layer), 8, 256, 256, 256, 256, 256, small,
+                                 ctypes.byref(d), None) == _lib.ERR_WORKSPACE
+    assert lib.fleet_moe_workspace_status(None, None, None) == _lib.ERR_ARG
