@@ -112,6 +112,10 @@ __global__ __launch_bounds__(kThreads) void router_topk_kernel(Params P) {
         const float l = s_logit[lane];
         if (P.logits) P.logits[(int64_t)t * kRouted + lane] = l;
         wave_softmax_topk(l, kRouted, kTopK, P.scaling, s_ids, s_w, P.bias);
+        // lanes < k read slots written by other lanes of this same wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
         if (lane < kTopK) {
             P.ids[(int64_t)t * kTopK + lane] = s_ids[lane];
             P.weights[(int64_t)t * kTopK + lane] = s_w[lane];

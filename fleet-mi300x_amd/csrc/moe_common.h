@@ -4,7 +4,8 @@
 //   * bf16 rounding is round-to-nearest-even on the fp32 bit pattern;
 //   * reductions whose result must be reproducible bit for bit (RMSNorm mean of
 //     squares, router logits, softmax) run in fp64 and are rounded once to fp32;
-//   * expert GEMVs accumulate in fp32 and reduce with a fixed butterfly.
+//   * expert GEMVs accumulate in fp32 and reduce in one fixed order (DPP
+//     row reductions, then the four rows in lane order).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -60,6 +61,22 @@ __device__ __forceinline__ float dot8(const u32x4& w, const float* x, float acc)
     return acc;
 }
 
+// bf16 pair dot with fp32 accumulation (v_dot2c_f32_bf16):
+// acc + a.lo * b.lo + a.hi * b.hi. The products of two bf16 values are exact.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+// 8-element dot of two 16-byte bf16 chunks through four dot2 steps.
+__device__ __forceinline__ float dot8_d2(const u32x4& w, const u32x4& x, float acc) {
+    acc = dot2(w.x, x.x, acc);
+    acc = dot2(w.y, x.y, acc);
+    acc = dot2(w.z, x.z, acc);
+    acc = dot2(w.w, x.w, acc);
+    return acc;
+}
+
 // Same, both operands bf16 chunks.
 __device__ __forceinline__ float dot8_bb(const u32x4& w, const u32x4& h, float acc) {
     acc = fmaf(bf_lo(w.x), bf_lo(h.x), acc);
@@ -73,23 +90,58 @@ __device__ __forceinline__ float dot8_bb(const u32x4& w, const u32x4& h, float a
     return acc;
 }
 
-// Fixed butterfly over the 64 lanes: every lane ends with the same sum, and
-// the order of additions never changes, so results are bitwise reproducible.
+// Wave reductions with DPP row operations (a few cycles each, no LDS
+// round trip): xor-1 and xor-2 quad permutes, the half-row and row mirrors
+// leave every lane of a 16-lane row holding the row sum, and the four row
+// sums are added in a fixed order through v_readlane. Every lane returns the
+// same value and the order of additions never changes, so results are
+// bitwise reproducible.
+#define FLEET_DPP(v, ctrl) __builtin_amdgcn_update_dpp(0, (v), (ctrl), 0xF, 0xF, false)
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = kLanes / 2; off; off >>= 1) v += __shfl_xor(v, off, kLanes);
-    return v;
+    v += __int_as_float(FLEET_DPP(__float_as_int(v), 0xB1));   // quad_perm [1,0,3,2]
+    v += __int_as_float(FLEET_DPP(__float_as_int(v), 0x4E));   // quad_perm [2,3,0,1]
+    v += __int_as_float(FLEET_DPP(__float_as_int(v), 0x141));  // row_half_mirror
+    v += __int_as_float(FLEET_DPP(__float_as_int(v), 0x140));  // row_mirror
+    const int b = __float_as_int(v);
+    return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) +
+            __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+           (__int_as_float(__builtin_amdgcn_readlane(b, 32)) +
+            __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ double dpp64(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = FLEET_DPP((int)(b & 0xffffffffll), kCtrl);
+    const int hi = FLEET_DPP((int)(b >> 32), kCtrl);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ __forceinline__ double readlane64(double v, int lane) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 __device__ __forceinline__ double wave_sum64(double v) {
-#pragma unroll
-    for (int off = kLanes / 2; off; off >>= 1) v += __shfl_xor(v, off, kLanes);
-    return v;
+    v += dpp64<0xB1>(v);
+    v += dpp64<0x4E>(v);
+    v += dpp64<0x141>(v);
+    v += dpp64<0x140>(v);
+    return (readlane64(v, 0) + readlane64(v, 16)) + (readlane64(v, 32) + readlane64(v, 48));
 }
-__device__ __forceinline__ double wave_max64(double v) {
-#pragma unroll
-    for (int off = kLanes / 2; off; off >>= 1) v = fmax(v, __shfl_xor(v, off, kLanes));
-    return v;
+
+__device__ __forceinline__ int wave_max_i(int v) {
+    v = max(v, FLEET_DPP(v, 0xB1));
+    v = max(v, FLEET_DPP(v, 0x4E));
+    v = max(v, FLEET_DPP(v, 0x141));
+    v = max(v, FLEET_DPP(v, 0x140));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
+
+// Value of lane 0 in every lane (all lanes must be active).
+__device__ __forceinline__ int wave_bcast(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Correctly rounded fp32 square root. The hardware square root is within one
 // ulp; the candidate is corrected by comparing `a` with the squares of the
@@ -124,60 +176,45 @@ __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Whole-wave wait until flags[0..n) all equal `target` (n <= 256), then an
-// agent-scope acquire. Returns false (after recording `reason` in *abort)
-// when the bound runs out or another wave already aborted.
-__device__ inline bool wave_wait_flags(const uint32_t* flags, int n, uint32_t target,
-                                       uint32_t* abort_word, uint32_t reason) {
-    const int lane = threadIdx.x & (kLanes - 1);
-    for (uint32_t it = 0;; ++it) {
-        bool ok = true;
-        for (int i = lane; i < n; i += kLanes) ok &= ld_agent(flags + i) == target;
-        if (__all(ok)) break;
-        if (it >= kSpinLimit || ld_agent(abort_word) != 0) {
-            if (lane == 0) __hip_atomic_fetch_or(abort_word, reason, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-            return false;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return true;
+// Softmax over one logit per lane (lanes >= n are padding) and greedy top-k
+// with ties to the lowest index, for one whole wave, entirely in registers:
+//   z = fp32(logit + bias), m = max z, e = exp(z - m) in fp64,
+//   p = fp32(e / sum e) (sum in the fixed DPP order),
+//   then k passes of: the wave max of p (exact in any order), a ballot of the
+//   lanes holding it, the lowest such lane wins the slot and drops out.
+// Selection rule of select_experts_from (src/kernels/fleet_kernel.hip:
+// 469-494: highest p, equal p to the lower index, unnormalised weights).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(FLEET_DPP(__float_as_int(v), 0xB1)));
+    v = fmaxf(v, __int_as_float(FLEET_DPP(__float_as_int(v), 0x4E)));
+    v = fmaxf(v, __int_as_float(FLEET_DPP(__float_as_int(v), 0x141)));
+    v = fmaxf(v, __int_as_float(FLEET_DPP(__float_as_int(v), 0x140)));
+    const int b = __float_as_int(v);
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)),
+                       __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)),
+                       __int_as_float(__builtin_amdgcn_readlane(b, 48))));
 }
 
-// Softmax in fp64 over one logit per lane (lanes >= n hold -inf) and greedy
-// top-k with ties to the lowest index: k passes of a butterfly argmax over
-// (p, lane). Writes ids[0..k) and p[ids] * scaling to LDS arrays on lane 0's
-// side (every lane computes the same values; lanes < k store slot `lane`).
-// Rule of select_experts_from, src/kernels/fleet_kernel.hip:469-494.
 __device__ inline void wave_softmax_topk(float logit, int n, int k, float scaling,
                                          int* ids_out, float* w_out, const float* bias) {
     const int lane = threadIdx.x & (kLanes - 1);
     const bool valid = lane < n;
-    // A bias is added in fp32 (z = fp32(logit + bias)); the softmax is fp64.
-    const float z32 = valid ? (bias ? logit + bias[lane] : logit) : 0.f;
-    const double zz = valid ? (double)z32 : -INFINITY;
-    const double mx = wave_max64(zz);
-    const double e = valid ? exp(zz - mx) : 0.0;
-    const double s = wave_sum64(e);
-    float p = valid ? (float)(e / s) : -INFINITY;
-    int my_slot = -1;
-    float my_val = 0.f;
+    const float z = valid ? (bias ? logit + bias[lane] : logit) : -INFINITY;
+    const float m = wave_max(z);
+    const double e = valid ? exp((double)z - (double)m) : 0.0;
+    const double sum = wave_sum64(e);
+    const float p = valid ? (float)(e / sum) : -INFINITY;
+    float q = p;
     for (int j = 0; j < k; ++j) {
-        float bv = p;
-        int bi = valid ? lane : 0x7fffffff;
-#pragma unroll
-        for (int off = kLanes / 2; off; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, kLanes);
-            const int oi = __shfl_xor(bi, off, kLanes);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        const float best = wave_max(q);
+        const unsigned long long hit = __ballot(q == best);
+        const int sel = (int)__builtin_ctzll(hit);     // lowest lane holding the max
+        if (lane == 0) {
+            ids_out[j] = sel;
+            w_out[j] = best * scaling;
         }
-        if (lane == j) { my_slot = bi; my_val = bv; }
-        if (lane == bi) p = -INFINITY;
-    }
-    if (lane < k) {
-        ids_out[lane] = my_slot;
-        w_out[lane] = my_val * scaling;
+        if (lane == sel) q = -INFINITY;
     }
 }
 

@@ -1,7 +1,7 @@
 // Batch-1 MoE layer for DeepSeek-V2-Lite on MI355X (gfx950): RMSNorm, router,
 // greedy top-6, six routed SwiGLU experts, the merged shared expert, the
 // weighted combine and the bf16 residual add, in ONE launch of 256
-// workgroups (one per CU).
+// workgroups (one per CU, 8 waves each).
 //
 // What it replaces in the reference: the NORM_ROUTER / EXPERT_GATE_UP /
 // EXPERT_DOWN task bodies of the persistent decode kernel
@@ -10,32 +10,37 @@
 // in the next layer's prologue (fleet_kernel.hip:146-201). The reference
 // gives each of its 8 XCDs one 17.3 MB "unit" and synchronises with XCD-local
 // and global events; this kernel spreads every gate/up row pair of all seven
-// experts over all 256 CUs and orders the work so that a CU always has
-// weight loads in flight while it waits on a dependency:
+// experts over all 256 CUs and keeps cross-CU communication off the critical
+// path:
 //
+//   routing: every workgroup computes all 64 router logits itself from L2
+//     (bf16 dot2, fp32 accumulate) together with a rigorous error bound, and
+//     selects the top 6. If the gap between the 6th and 7th logit exceeds
+//     twice the bound, that set is provably the exact one and routed
+//     streaming starts at once; otherwise (a near tie, ~1% of tokens) the
+//     workgroup waits for the exact logits below. Independently, the control
+//     wave of workgroups 0..63 computes one router row exactly (fp64 sum of
+//     the exact bf16 x bf16 products, rounded once) and publishes it; the
+//     routing weights and the slot order come from those exact logits, and
+//     they are only needed at the final combine.
 //   phase G (gate/up): the 11,264 row pairs of [shared | routed slot 0..5]
 //     are dealt round-robin to the 256 workgroups (44 pairs each, the first
-//     11 of them shared). Shared pairs come first: they do not depend on the
-//     routing, so they stream while 64 workgroups compute one router row
-//     each. Inside a workgroup, 8 waves pull pairs from an LDS ticket and
-//     double-buffer them (the next pair's 8 KB is in flight while the
-//     current one is reduced). A pair is 8 x 16-byte non-temporal loads per
-//     lane against x_norm held in registers;
+//     11 of them shared and routing-independent). Seven streaming waves pull
+//     pairs from an LDS ticket; a pair is 8 x 16-byte non-temporal loads per
+//     lane against x_norm (bf16 pairs in registers);
 //     h = bf16(bf16(silu(bf16(g))) * bf16(u)).
 //   phase D (down + combine): workgroup w owns output rows [8w, 8w+8). Waves
 //     0..5 take routed slot 0..5 for the 8 rows (8 x 2,816 B), waves 6..7 the
 //     shared expert's rows (4 x 5,632 B each): 22.5 KB per wave, issued
-//     before the wave waits for its unit's h, so the gate/up -> down
-//     dependency is hidden behind in-flight loads. The seven row dots of a
-//     row are combined in the owning workgroup's LDS in one fixed order: no
-//     partial buffers, no float atomics.
+//     before the wave waits for its unit's h. The seven row dots of a row are
+//     combined in the owning workgroup's LDS in one fixed order: no partial
+//     buffers, no float atomics.
 //
 // Cross-workgroup data is self-validating: every h value is published as one
-// 32-bit word (epoch tag << 16 | bf16 h) and every router logit as one 64-bit
-// word (epoch << 32 | fp32 bits), written and read with device-scope
+// 32-bit word (epoch tag << 16 | bf16 h) and every exact router logit as one
+// 64-bit word (epoch << 32 | fp32 bits), written and read with device-scope
 // (sc1) accesses. A consumer polls the words it needs until every tag equals
-// the current call's epoch, so there are no flags, no release fences and no
-// L2 write-backs; the words of the previous call carry the previous epoch.
+// the current call's epoch: no flags, no release fences, no L2 write-backs.
 // The last workgroup to exit advances the epoch. Every wait is bounded and
 // records an abort reason instead of hanging.
 #include <stddef.h>
@@ -58,11 +63,20 @@ constexpr int kPairs = kSharedPairs + kTopK * kInter;   // 11264
 constexpr int kItems = kPairs / kWG;           // 44 pairs per workgroup
 constexpr int kSharedItems = kSharedPairs / kWG;   // 11
 constexpr int kRowsPerWG = kHidden / kWG;      // 8 output rows per workgroup
-constexpr int kRouterWave = kWaves - 1;        // wave that computes a router row
+constexpr int kCtlWave = kWaves - 1;           // control wave: exact router row, routing
+constexpr int kRouterRowsPerWave = kRouted / kWaves;   // 8 local router rows per wave
+constexpr int kSharedRowBytes = kSharedInter * 2;              // 5,632 B per shared down row
+constexpr int kSharedBlockBytes = kRowsPerWG * kSharedRowBytes;  // 45,056 B = 44 x 1 KB
+static_assert(kSharedBlockBytes % 1024 == 0, "shared down block is whole 1 KB wave loads");
 static_assert(kPairs % kWG == 0 && kSharedPairs % kWG == 0, "pair split");
 static_assert(kRowsPerWG == 8 && kWaves == 8, "down split assumes 8 rows x 8 waves");
-static_assert(kSharedItems >= kWaves, "every wave starts on a routing-independent pair");
-static_assert(kRouted <= kWG, "one router row per workgroup");
+static_assert(kSharedItems >= kWaves - 1, "streaming waves start on routing-independent pairs");
+static_assert(kRouted <= kWG, "one exact router row per workgroup");
+
+// Sticky status bit (beside the header's FLEET_MOE_ABORT_* bits): the locally
+// selected expert set disagreed with the exact logits. The margin test makes
+// this impossible; it is checked anyway.
+constexpr uint32_t kAbortRouteMismatch = 0x100u;
 
 // Device workspace (zero-filled once by the caller). The header keeps the
 // offsets fleet_moe_workspace_status relies on.
@@ -71,7 +85,7 @@ struct Workspace {
     uint32_t exits;        // workgroup exits over all calls
     uint32_t abort;        // sticky FLEET_MOE_ABORT_* bits
     uint32_t pad0[61];
-    uint64_t logit[kRouted];   // (epoch << 32) | fp32 logit bits
+    uint64_t logit[kRouted];   // (epoch << 32) | fp32 exact logit bits
     uint32_t h[kPairs];        // (epoch & 0xffff) << 16 | bf16 h; shared [0, 2816),
                                // routed slot k at 2816 + k * 1408
 };
@@ -97,7 +111,7 @@ struct Params {
     float eps;
     float scaling;
 #if FLEET_MOE_TRACE
-    unsigned long long* trace; // [kWG][kWaves][8] s_memrealtime stamps, or null
+    unsigned long long* trace; // [kWG][kWaves][16] s_memrealtime stamps, or null
 #endif
 };
 
@@ -105,7 +119,7 @@ struct Params {
 #define FLEET_TRACE(k)                                                                   \
     do {                                                                                 \
         if (P.trace && (threadIdx.x & 63) == 0)                                          \
-            P.trace[((size_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * 8 + (k)] =      \
+            P.trace[((size_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * 16 + (k)] =     \
                 __builtin_amdgcn_s_memrealtime();                                        \
     } while (0)
 #else
@@ -113,13 +127,19 @@ struct Params {
 #endif
 
 struct Lds {
-    float xn[kHidden];
+    alignas(16) uint32_t xb[kHidden / 2];  // x_norm as bf16 pairs
     double red[kWaves];
-    int ids[8];
-    float w[8];
+    double xsq[kWaves];
+    float llog[kRouted];       // local (fp32) logits
+    float lnrm[kRouted];       // local sum of squares of each router row
+    int ids[8];                // slot -> expert id (slot order = local selection order)
+    float w[8];                // slot -> routing weight (exact)
+    int order[8];              // exact selection order: order[j] = slot
     float part[kUnits][kRowsPerWG];
     int next;
-    int route;                 // 0 idle, 1 being fetched, 2 ready, 3 failed
+    int route;                 // 0 pending, 2 ready, 3 failed
+    int sdown_ready;           // the shared down rows have landed in sdown
+    alignas(16) uint8_t sdown[kSharedBlockBytes];   // this workgroup's 8 shared down rows
 };
 
 // Pair `j` of workgroup `wg`: shared pairs wg + 256 j for j < 11, then the
@@ -135,8 +155,6 @@ __device__ __forceinline__ void item_of(int wg, int j, int& unit, int& pair) {
     }
 }
 
-__device__ __forceinline__ int wave_bcast(int v) { return __shfl(v, 0, kLanes); }
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
 }
@@ -145,62 +163,149 @@ __device__ __forceinline__ u32x4 ld_dev16(__amdgpu_buffer_rsrc_t r, int byte_off
     return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16);
 }
 
-// First wave of the workgroup to need the routing fetches it: polls the 64
-// tagged router words (one per lane) until every tag is this call's epoch,
-// runs softmax + top-6 on this one wave, and publishes ids/weights to LDS.
-// Other waves wait on LDS.
-__device__ bool ensure_routing(const Params& P, Lds& L, uint32_t epoch) {
+// Polls the 64 exact router words (one per lane) until every tag is this
+// call's epoch; four polls in flight. Returns false if the bound ran out.
+__device__ bool poll_exact_logits(const Params& P, uint32_t epoch, float& logit) {
     const int lane = threadIdx.x & (kLanes - 1);
-    int st = __hip_atomic_load(&L.route, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (st >= 2) return st == 2;
-    int old = 0;
-    if (lane == 0) {
-        int expected = 0;
-        __hip_atomic_compare_exchange_strong(&L.route, &expected, 1, __ATOMIC_RELAXED,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        old = expected;
+    Workspace* ws = P.ws;
+    const uint64_t* src = &ws->logit[lane];
+    auto poll = [&]() {
+        return __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto ready = [&](uint64_t w) { return __all((uint32_t)(w >> 32) == epoch); };
+    uint64_t a = poll();
+    __builtin_amdgcn_s_sleep(4);
+    uint64_t b = poll();
+    __builtin_amdgcn_s_sleep(4);
+    uint64_t c = poll();
+    __builtin_amdgcn_s_sleep(4);
+    uint64_t d = poll();
+    for (uint32_t it = 0; it < kSpinLimit; it += 4) {
+        if (ready(a)) { logit = __uint_as_float((uint32_t)a); return true; }
+        __builtin_amdgcn_s_sleep(4);
+        a = poll();
+        if (ready(b)) { logit = __uint_as_float((uint32_t)b); return true; }
+        __builtin_amdgcn_s_sleep(4);
+        b = poll();
+        if (ready(c)) { logit = __uint_as_float((uint32_t)c); return true; }
+        __builtin_amdgcn_s_sleep(4);
+        c = poll();
+        if (ready(d)) { logit = __uint_as_float((uint32_t)d); return true; }
+        __builtin_amdgcn_s_sleep(4);
+        d = poll();
+        if ((it & 1023) == 1020 && ld_agent(&ws->abort) != 0) break;
     }
-    old = wave_bcast(old);
-    if (old == 0) {
-        Workspace* ws = P.ws;
-        uint64_t v = 0;
-        bool ok = false;
-        for (uint32_t it = 0;; ++it) {
-            v = __hip_atomic_load(&ws->logit[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (__all((uint32_t)(v >> 32) == epoch)) { ok = true; break; }
-            if (it >= kSpinLimit || ld_agent(&ws->abort) != 0) {
-                if (lane == 0)
-                    __hip_atomic_fetch_or(&ws->abort, FLEET_MOE_ABORT_ROUTER_WAIT,
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (ok) {
-            wave_softmax_topk(__uint_as_float((uint32_t)v), kRouted, kTopK, P.scaling, L.ids,
-                              L.w, nullptr);
-            if (lane < kTopK) {
-                L.ids[lane] = min(max(L.ids[lane], 0), kRouted - 1);
-                if (blockIdx.x == 0 && P.ids_out) P.ids_out[lane] = L.ids[lane];
-                if (blockIdx.x == 0 && P.w_out) P.w_out[lane] = L.w[lane];
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        if (lane == 0)
-            __hip_atomic_store(&L.route, ok ? 2 : 3, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-        return ok;
-    }
-    // Bounded because the fetching wave's own wait is bounded.
-    while ((st = __hip_atomic_load(&L.route, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP)) < 2)
-        __builtin_amdgcn_s_sleep(1);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    return st == 2;
+    if (lane == 0)
+        __hip_atomic_fetch_or(&ws->abort, FLEET_MOE_ABORT_ROUTER_WAIT, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    return false;
 }
 
-// Base of gate/up row pair `pair` of `unit`, as 16-byte chunks. ids were
-// clamped to [0, 64) when they were published.
+// a2 (exact): router row `row`, fp64 accumulation of the exact bf16 x bf16
+// products rounded once to fp32, published as a tagged 64-bit word.
+__device__ void publish_exact_row(const Params& P, const u32x4 (&er)[4], const u32x4 (&xq)[4],
+                                  int row, uint32_t epoch) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    double acc = 0.0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t wv[4] = {er[m].x, er[m].y, er[m].z, er[m].w};
+        const uint32_t xw[4] = {xq[m].x, xq[m].y, xq[m].z, xq[m].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc += (double)(bf_lo(wv[q]) * bf_lo(xw[q]));
+            acc += (double)(bf_hi(wv[q]) * bf_hi(xw[q]));
+        }
+    }
+    acc = wave_sum64(acc);
+    if (lane == 0)
+        __hip_atomic_store(&P.ws->logit[row], ((uint64_t)epoch << 32) | __float_as_uint((float)acc),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    FLEET_TRACE(8);
+}
+
+// Control wave, once the local logits are in LDS: top-7 by local logit (ties
+// to the lower index). The fp32 dot2 sum of a row differs from the exact dot
+// product by at most eps_row = 4 * 56 * 2^-24 * ||w_row||_2 * ||x_norm||_2
+// (at most 48 roundings along a lane's chain plus 8 in the reduction,
+// Cauchy-Schwarz for sum |w_i x_i|, a factor 4 of headroom). If the 6th-7th
+// gap exceeds twice the largest eps, the selected set equals the exact top 6
+// (and no softmax tie can reorder it: the gap is far above fp32 resolution);
+// otherwise the exact logits are fetched and selected from directly.
+__device__ bool select_routing(const Params& P, Lds& L, uint32_t epoch, float xnorm2,
+                               bool publish_row, const u32x4 (&er)[4], const u32x4 (&xq)[4],
+                               bool& exact) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const float l = L.llog[lane];
+    const float eps =
+        4.0f * 56.0f * 5.9604645e-8f * __fsqrt_rn(L.lnrm[lane]) * __fsqrt_rn(xnorm2);
+    const float eps_max = wave_max(eps);
+    float q = l;
+    float sel_val[7];
+    int sel_id[7];
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+        const float best = wave_max(q);
+        const unsigned long long hit = __ballot(q == best);
+        sel_id[j] = (int)__builtin_ctzll(hit);
+        sel_val[j] = best;
+        if (lane == sel_id[j]) q = -INFINITY;
+    }
+    exact = false;
+    if (sel_val[5] - sel_val[6] > 2.0f * eps_max) {
+        if (lane < kTopK) {
+            int id = sel_id[0];
+#pragma unroll
+            for (int j = 1; j < kTopK; ++j) id = lane == j ? sel_id[j] : id;
+            L.ids[lane] = id;
+        }
+        return true;
+    }
+    // Near tie: every workgroup reaches the same decision, so the row owners
+    // publish their exact rows before anyone waits for them.
+    exact = true;
+    if (publish_row) publish_exact_row(P, er, xq, blockIdx.x, epoch);
+    float el;
+    if (!poll_exact_logits(P, epoch, el)) return false;
+    wave_softmax_topk(el, kRouted, kTopK, P.scaling, L.ids, L.w, nullptr);
+    if (lane < kTopK) L.order[lane] = lane;
+    return true;
+}
+
+// Exact weights and order for a locally selected set: softmax of the exact
+// logits (fp64, as the standalone router computes it), then each slot's
+// weight and the slots sorted by (p descending, id ascending). Also checks
+// that the set is the exact top 6.
+__device__ void exact_weights(const Params& P, Lds& L, uint32_t epoch) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    float el;
+    if (!poll_exact_logits(P, epoch, el)) return;
+    const float m = wave_max(el);
+    const double e = exp((double)el - (double)m);
+    const double sum = wave_sum64(e);
+    const float p = (float)(e / sum);
+    const int pb = __float_as_int(p);
+    // rank of this lane's expert among all 64 by (p desc, index asc)
+    int rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < kLanes; ++j) {
+        const float o = __int_as_float(__builtin_amdgcn_readlane(pb, j));
+        rank += (o > p) || (o == p && j < lane);
+    }
+    // every lane takes part in the permutes; lanes < 6 use the result
+    const int id = lane < kTopK ? L.ids[lane] : 0;
+    const float pk = __int_as_float(__builtin_amdgcn_ds_bpermute(id << 2, pb));
+    const int rk = __builtin_amdgcn_ds_bpermute(id << 2, rank);
+    if (lane < kTopK) {
+        L.w[lane] = pk * P.scaling;
+        if (rk < kTopK) L.order[rk] = lane;
+        else __hip_atomic_fetch_or(&P.ws->abort, kAbortRouteMismatch, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Base of gate/up row pair `pair` of `unit`, as 16-byte chunks. ids are in
+// [0, 64) by construction (ballot lanes / softmax lanes).
 __device__ __forceinline__ const u32x4* pair_base(const Params& P, const Lds& L, int unit,
                                                   int pair) {
     const uint16_t* blk = unit == 0
@@ -219,14 +324,14 @@ __device__ __forceinline__ void issue_pair(const u32x4* base, int lane, u32x4 (&
 
 // Reduce one gate/up pair and publish its tagged h word.
 __device__ __forceinline__ void finish_pair(const Params& P, int unit, int pair,
-                                            const u32x4 (&b)[8], const float (&xr)[4][8],
+                                            const u32x4 (&b)[8], const u32x4 (&xq)[4],
                                             uint32_t tag) {
     const int lane = threadIdx.x & (kLanes - 1);
     float g = 0.f, u = 0.f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        g = dot8(b[m], xr[m], g);
-        u = dot8(b[4 + m], xr[m], u);
+        g = dot8_d2(b[m], xq[m], g);
+        u = dot8_d2(b[4 + m], xq[m], u);
     }
     g = wave_sum(g);
     u = wave_sum(u);
@@ -262,7 +367,7 @@ __device__ bool wait_h(const Params& P, int unit, int n_chunks, uint32_t tag,
             }
         }
         if (__all(ok)) return true;
-        if (it >= kSpinLimit || ld_agent(&P.ws->abort) != 0) {
+        if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&P.ws->abort) != 0)) {
             if (lane == 0)
                 __hip_atomic_fetch_or(&P.ws->abort, FLEET_MOE_ABORT_UNIT_WAIT, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
@@ -272,6 +377,17 @@ __device__ bool wait_h(const Params& P, int unit, int n_chunks, uint32_t tag,
     }
 }
 
+// Any wave that needs the routing waits for the control wave's LDS
+// publication (bounded, because the control wave's own waits are bounded).
+__device__ __forceinline__ bool wait_routing(Lds& L) {
+    int st;
+    while ((st = __hip_atomic_load(&L.route, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP)) < 2)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    return st == 2;
+}
+
 __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     __shared__ Lds L;
     const int wg = blockIdx.x;
@@ -279,29 +395,51 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     const int wave = tid >> 6;
     const int lane = tid & (kLanes - 1);
     Workspace* ws = P.ws;
+    const bool ctl = wave == kCtlWave;
 
-    // Issue order: x (needed first), the router row, then this wave's first
-    // (shared, routing-independent) pair.
+    // Issue order: x, this wave's first four local router rows (L2-resident
+    // after the first workgroup of an XCD touches them), the exact router row
+    // (control wave of workgroups 0..63), then each streaming wave's first
+    // shared pair.
     const float4 xv = reinterpret_cast<const float4*>(P.x)[tid];
-    const bool router_wave = wave == kRouterWave && wg < kRouted;
-    u32x4 rrow[4];
-    if (router_wave) {
-        const u32x4* r = P.router + (int64_t)wg * kRowChunks;
+    const int rrow0 = wave * kRouterRowsPerWave;
+    u32x4 ra[4][4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) rrow[m] = r[lane + kLanes * m];
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            ra[r][m] = P.router[(int64_t)(rrow0 + r) * kRowChunks + lane + kLanes * m];
+    const bool exact_row = ctl && wg < kRouted;
+    u32x4 er[4];
+    if (exact_row) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) er[m] = P.router[(int64_t)wg * kRowChunks + lane + kLanes * m];
     }
-    u32x4 bufA[8], bufB[8];
-    int cur = wave;
-    issue_pair(reinterpret_cast<const u32x4*>(P.shared) + (int64_t)(wg + kWG * cur) * 2 * kRowChunks,
-               lane, bufA);
+    // The control wave has no pair in flight: it streams this workgroup's
+    // eight shared-expert down rows (44 KB, routing-independent) straight
+    // into LDS while the routing is being settled.
+    if (ctl) {
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(
+                                 P.shared + (int64_t)2 * kSharedInter * kHidden) +
+                             (int64_t)wg * kSharedBlockBytes + lane * 16;
+#pragma unroll 4
+        for (int k = 0; k < kSharedBlockBytes / 1024; ++k)
+            __builtin_amdgcn_global_load_lds(src + k * 1024, L.sdown + k * 1024, 16, 0, 0);
+    }
+    u32x4 bufA[8];
+    int cur;
+    if (!ctl)
+        issue_pair(reinterpret_cast<const u32x4*>(P.shared) +
+                       (int64_t)(wg + kWG * wave) * 2 * kRowChunks,
+                   lane, bufA);
     const uint32_t epoch = ld_agent(&ws->epoch) + 1u;
     const uint32_t tag = (epoch & 0xffffu) << 16;
     FLEET_TRACE(0);
-    if (tid == 0) { L.next = kWaves; L.route = 0; }
-    if (tid < 8) { L.ids[tid] = 0; L.w[tid] = 0.f; }
+    if (tid == 0) { L.next = kWaves - 1; L.route = 0; L.sdown_ready = 0; }
+    if (tid < 8) { L.ids[tid] = 0; L.w[tid] = 0.f; L.order[tid] = tid; }
 
     // a1: RMSNorm of x (every workgroup, identical arithmetic): fp64 sum of
-    // squares in a fixed tree, var = fp32(ssq / H), inv = 1 / sqrt(var + eps)
+    // squares in a fixed order, var = fp32(ssq / H), inv = 1 / sqrt(var + eps)
     // in correctly rounded fp32, y = bf16(bf16(x * inv) * gamma).
     double ss = (double)xv.x * xv.x + (double)xv.y * xv.y + (double)xv.z * xv.z +
                 (double)xv.w * xv.w;
@@ -313,90 +451,134 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     for (int w = 0; w < kWaves; ++w) ssq += L.red[w];
     const float var = (float)(ssq / (double)kHidden);
     const float inv = __fdiv_rn(1.0f, sqrt_rn(var + P.eps));
-    {
-        float y[4] = {bf16r(xv.x * inv), bf16r(xv.y * inv), bf16r(xv.z * inv), bf16r(xv.w * inv)};
-        if (P.norm) {
-            const uint2 gb = reinterpret_cast<const uint2*>(P.norm)[tid];
-            y[0] = bf16r(y[0] * bf_lo(gb.x));
-            y[1] = bf16r(y[1] * bf_hi(gb.x));
-            y[2] = bf16r(y[2] * bf_lo(gb.y));
-            y[3] = bf16r(y[3] * bf_hi(gb.y));
-        }
-        reinterpret_cast<float4*>(L.xn)[tid] = make_float4(y[0], y[1], y[2], y[3]);
+    float y[4] = {bf16r(xv.x * inv), bf16r(xv.y * inv), bf16r(xv.z * inv), bf16r(xv.w * inv)};
+    if (P.norm) {
+        const uint2 gb = reinterpret_cast<const uint2*>(P.norm)[tid];
+        y[0] = bf16r(y[0] * bf_lo(gb.x));
+        y[1] = bf16r(y[1] * bf_hi(gb.x));
+        y[2] = bf16r(y[2] * bf_lo(gb.y));
+        y[3] = bf16r(y[3] * bf_hi(gb.y));
     }
+    L.xb[2 * tid] = bf16_bits(y[0]) | (bf16_bits(y[1]) << 16);
+    L.xb[2 * tid + 1] = bf16_bits(y[2]) | (bf16_bits(y[3]) << 16);
+    {
+        const double q = (double)y[0] * y[0] + (double)y[1] * y[1] + (double)y[2] * y[2] +
+                         (double)y[3] * y[3];
+        const double qs = wave_sum64(q);
+        if (lane == 0) L.xsq[wave] = qs;
+    }
+    // the second half of this wave's local router rows
+    u32x4 rb[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            rb[r][m] = P.router[(int64_t)(rrow0 + 4 + r) * kRowChunks + lane + kLanes * m];
     __syncthreads();
-    float xr[4][8];
+    u32x4 xq[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xr[m][i] = L.xn[kChunk * (lane + kLanes * m) + i];
+        xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
     FLEET_TRACE(1);
 
-    // a2: one router row per workgroup (fp64 accumulation of the exact
-    // bf16 x bf16 products), published as a tagged 64-bit word.
-    if (router_wave) {
-        double acc = 0.0;
+    // a2 (local): eight router rows per wave, dot2 with fp32 accumulation,
+    // plus each row's sum of squares for the error bound.
+    {
+        float lg[8], nr[8];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const uint32_t wv[4] = {rrow[m].x, rrow[m].y, rrow[m].z, rrow[m].w};
+        for (int r = 0; r < 4; ++r) {
+            float a = 0.f, n = 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc += (double)(bf_lo(wv[q]) * xr[m][2 * q]);
-                acc += (double)(bf_hi(wv[q]) * xr[m][2 * q + 1]);
+            for (int m = 0; m < 4; ++m) {
+                a = dot8_d2(ra[r][m], xq[m], a);
+                n = dot8_d2(ra[r][m], ra[r][m], n);
             }
+            lg[r] = wave_sum(a);
+            nr[r] = wave_sum(n);
         }
-        acc = wave_sum64(acc);
-        if (lane == 0)
-            __hip_atomic_store(&ws->logit[wg],
-                               ((uint64_t)epoch << 32) | __float_as_uint((float)acc),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float a = 0.f, n = 0.f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                a = dot8_d2(rb[r][m], xq[m], a);
+                n = dot8_d2(rb[r][m], rb[r][m], n);
+            }
+            lg[4 + r] = wave_sum(a);
+            nr[4 + r] = wave_sum(n);
+        }
+        if (lane < kRouterRowsPerWave) {
+            float lv = lg[0], nv = nr[0];
+#pragma unroll
+            for (int r = 1; r < 8; ++r) {
+                lv = lane == r ? lg[r] : lv;
+                nv = lane == r ? nr[r] : nv;
+            }
+            L.llog[rrow0 + lane] = lv;
+            L.lnrm[rrow0 + lane] = nv;
+        }
     }
 
-    // Phase G: gate/up pairs, double-buffered.
-    auto grab = [&]() {
+    __syncthreads();
+
+    // Pairs of this workgroup are handed out by an LDS ticket.
+    auto claim = [&]() -> int {
         int t = 0;
         if (lane == 0)
             t = __hip_atomic_fetch_add(&L.next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        return wave_bcast(t);
+        t = wave_bcast(t);
+        return t < kItems ? t : -1;
     };
-    bool traced_route = false;
-    auto issue = [&](int j, u32x4 (&b)[8]) {
+    auto issue = [&](int item, u32x4 (&b)[8]) {
         int u, p;
-        item_of(wg, j, u, p);
-        if (u != 0 && ensure_routing(P, L, epoch) && !traced_route) {
-            FLEET_TRACE(2);
-            traced_route = true;
-        }
+        item_of(wg, item, u, p);
+        if (u != 0) wait_routing(L);
         issue_pair(pair_base(P, L, u, p), lane, b);
     };
-    auto finish = [&](int j, const u32x4 (&b)[8]) {
+    auto finish = [&](int item, const u32x4 (&b)[8]) {
         int u, p;
-        item_of(wg, j, u, p);
-        finish_pair(P, u, p, b, xr, tag);
+        item_of(wg, item, u, p);
+        finish_pair(P, u, p, b, xq, tag);
     };
-    while (true) {
-        int nxt = grab();
-        if (nxt < kItems) issue(nxt, bufB);
+    bool exact_sel = false;
+    cur = ctl ? -1 : wave;
+    if (ctl) {
+        __builtin_amdgcn_s_setprio(2);
+        double xs = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) xs += L.xsq[w];
+        const bool ok = select_routing(P, L, epoch, (float)xs * 1.0001f, exact_row, er, xq,
+                                       exact_sel);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0)
+            __hip_atomic_store(&L.route, ok ? 2 : 3, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        __builtin_amdgcn_s_setprio(0);
+        FLEET_TRACE(10);
+        if (exact_row && !exact_sel) publish_exact_row(P, er, xq, wg, epoch);
+        cur = claim();
+        if (cur >= 0) issue(cur, bufA);
+    }
+    FLEET_TRACE(2);
+
+    // Phase G: gate/up pairs, one in flight per streaming wave.
+    while (cur >= 0) {
+        const int nxt = claim();
         finish(cur, bufA);
-        if (nxt >= kItems) break;
-        cur = nxt;
-        nxt = grab();
-        if (nxt < kItems) issue(nxt, bufA);
-        finish(cur, bufB);
-        if (nxt >= kItems) break;
+        if (nxt >= 0) issue(nxt, bufA);
         cur = nxt;
     }
     FLEET_TRACE(3);
 
-    // Phase D: this wave's down rows, all loads in flight before the wait.
+    // Phase D: this workgroup's 8 output rows. Waves 0..5 stream routed slot
+    // 0..5's rows (8 x 2,816 B), all loads in flight before the wave waits for
+    // its unit's h; waves 6..7 take the shared expert's rows from LDS.
     const int row0 = wg * kRowsPerWG;
-    u32x4 W[24];
     const bool routed = wave < kTopK;
     const int unit = routed ? 1 + wave : 0;
-    float wk = 0.f;
     if (routed) {
-        ensure_routing(P, L, epoch);
-        wk = L.w[wave];
+        wait_routing(L);
+        u32x4 W[24];
         const u32x4* base = reinterpret_cast<const u32x4*>(
                                 P.experts + (int64_t)L.ids[wave] * P.expert_stride +
                                 (int64_t)2 * kInter * kHidden) +
@@ -409,22 +591,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
                 W[3 * r + m] = c < kInterChunks ? ld_stream(base + r * kInterChunks + c)
                                                 : u32x4{0u, 0u, 0u, 0u};
             }
-    } else {
-        const int r0 = row0 + 4 * (wave - kTopK);
-        const u32x4* base = reinterpret_cast<const u32x4*>(
-                                P.shared + (int64_t)2 * kSharedInter * kHidden) +
-                            (int64_t)r0 * kSharedChunks;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int m = 0; m < 6; ++m) {
-                const int c = lane + kLanes * m;
-                W[6 * r + m] = c < kSharedChunks ? ld_stream(base + r * kSharedChunks + c)
-                                                 : u32x4{0u, 0u, 0u, 0u};
-            }
-    }
-    FLEET_TRACE(4);
-    if (routed) {
+        FLEET_TRACE(4);
         u32x4 H[3];
         wait_h<3>(P, unit, kInterChunks, tag, H);
         FLEET_TRACE(5);
@@ -432,36 +599,69 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         for (int r = 0; r < 8; ++r) {
             float acc = 0.f;
 #pragma unroll
-            for (int m = 0; m < 3; ++m) acc = dot8_bb(W[3 * r + m], H[m], acc);
+            for (int m = 0; m < 3; ++m) acc = dot8_d2(W[3 * r + m], H[m], acc);
             acc = wave_sum(acc);
-            if (lane == 0) L.part[unit][r] = bf16r(wk * bf16r(acc));
+            if (lane == 0) L.part[unit][r] = bf16r(acc);
         }
     } else {
+        if (ctl) {
+            // exact weights and order (the exact logits were published early)
+            if (!exact_sel && __hip_atomic_load(&L.route, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP) == 2)
+                exact_weights(P, L, epoch);
+            FLEET_TRACE(9);
+            // the shared down rows this wave put in flight at the start
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            if (lane == 0)
+                __hip_atomic_store(&L.sdown_ready, 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+            while (__hip_atomic_load(&L.sdown_ready, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+                __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
+        FLEET_TRACE(4);
         u32x4 H[6];
         wait_h<6>(P, unit, kSharedChunks, tag, H);
         FLEET_TRACE(5);
+        const int rs = 4 * (wave - kTopK);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            const u32x4* wr = reinterpret_cast<const u32x4*>(L.sdown + (rs + r) * kSharedRowBytes);
             float acc = 0.f;
 #pragma unroll
-            for (int m = 0; m < 6; ++m) acc = dot8_bb(W[6 * r + m], H[m], acc);
+            for (int m = 0; m < 6; ++m) {
+                const int c = lane + kLanes * m;
+                if (c < kSharedChunks) acc = dot8_d2(wr[c], H[m], acc);
+            }
             acc = wave_sum(acc);
-            if (lane == 0) L.part[0][4 * (wave - kTopK) + r] = bf16r(acc);
+            if (lane == 0) L.part[0][rs + r] = bf16r(acc);
         }
     }
     FLEET_TRACE(6);
     __syncthreads();
 
-    // a7: combine in slot order, then the bf16 residual add.
+    // a7: bf16(w_k * d_k) summed in exact selection order, then the shared
+    // expert and the bf16 residual add.
     if (tid < kRowsPerWG) {
         const int n = row0 + tid;
         float y = 0.f;
 #pragma unroll
-        for (int k = 0; k < kTopK; ++k) y += L.part[1 + k][tid];
+        for (int j = 0; j < kTopK; ++j) {
+            const int k = L.order[j];
+            y += bf16r(L.w[k] * L.part[1 + k][tid]);
+        }
         const float out = bf16r(bf16r(y) + L.part[0][tid]);
         const float xo = bf16r(P.x[n] + out);
         P.x_out[n] = xo;
         if (P.moe_out) P.moe_out[n] = (uint16_t)bf16_bits(out);
+    }
+    if (wg == 0 && tid < kTopK) {
+        const int k = L.order[tid];
+        if (P.ids_out) P.ids_out[tid] = L.ids[k];
+        if (P.w_out) P.w_out[tid] = L.w[k];
     }
     if (tid == 0) {
         const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
