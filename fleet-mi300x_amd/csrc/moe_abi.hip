@@ -124,6 +124,33 @@ __global__ __launch_bounds__(kThreads) void router_topk_kernel(Params P) {
 }
 
 }  // namespace router
+
+namespace probe {
+
+// Streaming read with the weight-load pattern of the MoE kernels: each wave
+// reads 4 contiguous 1 KB wave-loads (16-byte non-temporal loads per lane)
+// per step, grid-stride. The XOR of everything read is written only if it
+// equals an improbable constant, so the loads cannot be dropped.
+constexpr int kThreads = 256;
+constexpr int kDepth = 4;
+__global__ __launch_bounds__(kThreads) void stream_read_kernel(const u32x4* __restrict__ p,
+                                                               size_t n16, uint32_t* sink) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const size_t wave = (blockIdx.x * (size_t)kThreads + threadIdx.x) / kLanes;
+    const size_t nwaves = (gridDim.x * (size_t)kThreads) / kLanes;
+    const size_t tile = (size_t)kDepth * kLanes;
+    uint32_t acc = 0;
+    for (size_t t = wave * tile; t < n16; t += nwaves * tile) {
+        u32x4 v[kDepth];
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) v[d] = ld_stream(p + t + d * kLanes + lane);
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+}  // namespace probe
 }  // namespace fleet_moe
 
 using namespace fleet_moe;
@@ -155,6 +182,21 @@ extern "C" int fleet_moe_router_topk(const uint16_t* w_router, const float* x_no
     P.scaling = dims->routed_scaling;
     hipLaunchKernelGGL(router::router_topk_kernel, dim3(n_tokens), dim3(router::kThreads), 0,
                        stream, P);
+    return (int)hipGetLastError();
+}
+
+extern "C" int fleet_moe_stream_read(const void* buf, size_t bytes, uint32_t* sink,
+                                     hipStream_t stream) {
+    if (!buf || !sink || !aligned(buf, 16) || !aligned(sink, 4) || bytes == 0 ||
+        bytes % (16 * kLanes * probe::kDepth) != 0)
+        return FLEET_MOE_ERR_ARG;
+    if (int e = check_device_impl(1)) return e;
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(probe::stream_read_kernel, dim3(2 * cus), dim3(probe::kThreads), 0, stream,
+                       static_cast<const u32x4*>(buf), bytes / 16, sink);
     return (int)hipGetLastError();
 }
 

@@ -47,6 +47,7 @@ SYMBOLS = [
     ("fleet_moe_grouped", c_int,
      [POINTER(FleetMoeLayer), c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
       c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_moe_stream_read", c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
     ("fleet_moe_workspace_status", c_int, [c_void_p, POINTER(c_uint32), c_void_p]),
     ("fleet_moe_error_string", c_char_p, [c_int]),
     ("fleet_moe_abi_version", c_int, []),

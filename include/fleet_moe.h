@@ -124,6 +124,15 @@ int fleet_moe_workspace_status(const void* workspace, uint32_t* status, hipStrea
 #define FLEET_MOE_ABORT_UNIT_WAIT 0x2u    /* an expert unit never completed */
 #define FLEET_MOE_ABORT_GROUP_WAIT 0x4u   /* grouped step phase never completed */
 
+/* Diagnostic: reads `bytes` of device memory with the weight-streaming load
+ * pattern of the kernels above (16-byte non-temporal loads, 1 KB per wave
+ * instruction) and nothing else. Gives the achievable HBM read rate, and is
+ * the known-size kernel against which rocprofv3 FETCH_SIZE is calibrated.
+ * The reference's equivalent is bench/microbench.hip section (c),
+ * gemv_stream (:422-447). bytes must be a multiple of 4096; sink: a device
+ * uint32 that is written only if the XOR of the data is 0x9e3779b9. */
+int fleet_moe_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream);
+
 /* Human-readable text for a return code of this library. */
 const char* fleet_moe_error_string(int code);
 
