@@ -47,9 +47,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true")
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="also run a plain device copy of this many MiB (a known-size "
-                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run the known-size kernels that scale rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE: fleet_moe_stream_read over 256 MiB and a 64 MiB fill, "
+                         "3 launches each")
     return ap.parse_args()
 
 
@@ -214,19 +215,48 @@ def main() -> int:
 
     if not args.no_grouped:
         result["grouped"] = bench_grouped(torch, dev, stream, layer, dims, x_host)
-    if args.copy_calibration_mib:
-        n = args.copy_calibration_mib << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
+    result["stream_read"] = stream_ceiling(torch, dev, stream, lib)
+    if args.calibrate:
+        n = 256 << 20
+        buf = torch.ones(n // 4, dtype=torch.int32, device=dev)
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
         for _ in range(3):
-            dst.copy_(src)
+            _lib.check(lib.fleet_moe_stream_read(buf.data_ptr(), n, sink.data_ptr(), sh),
+                       "fleet_moe_stream_read")
+        fill = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        for _ in range(3):
+            fill.fill_(3)
         torch.cuda.synchronize()
-        result["copy_calibration_bytes"] = n
+        result["calibration"] = {"stream_read_bytes": n, "fill_bytes": 64 << 20, "launches": 3}
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(blob, lay, x_host[:K], args.cpu_seconds, gpu_ids)
     print(json.dumps(result), flush=True)
     return 0 if status == 0 else 1
+
+
+def stream_ceiling(torch, dev, stream, lib):
+    """Achievable HBM read rate with the kernels' load pattern: the streaming
+    probe over 2 GiB (far beyond the 256 MB of L2 + MALL), best of 10."""
+    from fleet_moe import _lib
+    n = 2 << 30
+    buf = torch.ones(n // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    sh = int(stream.cuda_stream)
+    best = float("inf")
+    for i in range(12):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        _lib.check(lib.fleet_moe_stream_read(buf.data_ptr(), n, sink.data_ptr(), sh),
+                   "fleet_moe_stream_read")
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 2:
+            best = min(best, a.elapsed_time(b) * 1e-3)
+    del buf
+    return {"bytes": n, "gbs": round(n / best / 1e9, 1), "frac_of_peak": round(n / best / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel": "fleet_moe::probe::stream_read_kernel"}
 
 
 def bench_grouped(torch, dev, stream, layer, dims, x_host):

@@ -145,3 +145,89 @@ def test_decode_in_place_repeatable_and_zero_input(dev):
     np.testing.assert_array_equal(z["ids"].cpu().numpy(), np.arange(6))
     assert not torch.any(z["x_out"] != 0)
     assert dec.status() == 0
+
+
+class _RouterSwap:
+    """A DeviceLayer with its router pointer replaced (duck-typed for
+    LayerDecoder.decode_into, which only asks for c_layer())."""
+
+    def __init__(self, base, router_dev):
+        self.base, self.router_dev = base, router_dev
+
+    def c_layer(self):
+        cl = self.base.c_layer()
+        cl.router = self.router_dev.data_ptr()
+        return cl
+
+
+def test_decode_exact_tie_takes_the_exact_routing_path(dev):
+    """Copy the router row of the 6th-ranked expert over the 7th-ranked one:
+    the two logits are then exactly equal, the kernel's local selection cannot
+    separate them (gap 0 < the error bound), so it must fall back to the
+    exact logits and break the tie to the lower index, as the oracle does."""
+    import dataclasses
+    layer, pl = dev
+    pl.widen()
+    dec = ops.LayerDecoder(DSV2_LITE)
+    cases = 0
+    for seed in (50, 51, 52):
+        x = synth.hidden_inputs(seed, 1)[0]
+        want0 = orc.moe_layer(pl, x)
+        order = np.lexsort((np.arange(64), -want0["logits"].astype(np.float64)))
+        e6, e7 = int(order[5]), int(order[6])
+        router = pl.router.reshape(64, -1).copy()
+        router[e7] = router[e6]
+        pl2 = dataclasses.replace(pl, router=router.reshape(pl.router.shape))
+        want = orc.moe_layer(pl2, x)
+        lo = want["logits"]
+        assert lo[e6] == lo[e7]
+        assert min(e6, e7) in want["ids"] and max(e6, e7) not in want["ids"]
+        rdev = torch.from_numpy(router.view(np.int16).reshape(-1)).cuda()
+        say(f"decode exact tie seed={seed} experts {e6}/{e7}")
+        got = dec.decode(_RouterSwap(layer, rdev), torch.from_numpy(x).cuda())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got["ids"].cpu().numpy(), want["ids"])
+        np.testing.assert_array_equal(got["weights"].cpu().numpy().view(np.uint32),
+                                      want["weights"].view(np.uint32))
+        assert rel_err(got["x_out"].cpu().numpy(), want["x_out"]) <= REL_TOL
+        cases += 1
+    assert cases == 3 and dec.status() == 0
+
+
+def test_decode_graph_replay_matches_eager(dev):
+    """Four decode launches captured in one HIP graph and replayed three times,
+    with eager launches on the same workspace in between: every replay equals
+    the eager result bit for bit (the workspace is never memset; the call
+    epoch lives in it)."""
+    layer, _ = dev
+    dec = ops.LayerDecoder(DSV2_LITE)
+    n = 4
+    x = torch.from_numpy(orc.bf16_round(synth.hidden_inputs(60, n))).cuda()
+    ref = torch.empty_like(x)
+    ref_ids = torch.empty((n, 6), dtype=torch.int32, device="cuda")
+    for t in range(n):
+        dec.decode_into(layer, x[t], ref[t], ids=ref_ids[t])
+    out = torch.empty_like(x)
+    ids = torch.empty_like(ref_ids)
+    say("graph capture of 4 decode launches")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for t in range(n):
+                dec.decode_into(layer, x[t], out[t], ids=ids[t])
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    extra = torch.from_numpy(synth.hidden_inputs(61, 1)[0]).cuda()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        ids.fill_(-1)
+        torch.cuda.synchronize()
+        say(f"graph replay {rep}")
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(ids, ref_ids), f"replay {rep}"
+        dec.decode(layer, extra)          # eager work on the same workspace between replays
+        torch.cuda.synchronize()
+    assert dec.status() == 0
