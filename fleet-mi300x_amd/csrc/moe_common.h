@@ -176,6 +176,75 @@ __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Buffer resource over a device buffer (raw, 32-bit byte offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+// 16-byte device-scope (sc1) load: sees the latest values written by any CU
+// with device-scope stores, whatever this CU's caches hold.
+__device__ __forceinline__ u32x4 ld_dev16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16);
+}
+
+// Multi-value wave reduction: N values per lane (N a power of two <= 64) are
+// summed over the 64 lanes in six exchange steps, lane L with lane L ^ a_k for
+// a = {1, 2, 7, 15, 16, 32} (DPP quad_perm x2, row_half_mirror, row_mirror,
+// ds_swizzle, ds_bpermute). In each of the first log2(N) steps a lane keeps
+// half of its values (the upper half when parity(L & f_k) = 1, f = {5, 6, 12,
+// 8, 16, 32}, the dual basis of a) and adds its partner's copy of that half;
+// the remaining steps add the single value. On return v[0] of every lane holds
+// the wave total of value msum_index<N>(L); the lanes sharing an index hold
+// bitwise equal totals (each addition pairs the same two operands). Cost:
+// about 1.5 N + 6 DPP adds, against 11 N for N separate wave sums.
+template <int K>
+__device__ __forceinline__ float msum_xchg(float x) {
+    if constexpr (K == 0) return __int_as_float(FLEET_DPP(__float_as_int(x), 0xB1));
+    else if constexpr (K == 1) return __int_as_float(FLEET_DPP(__float_as_int(x), 0x4E));
+    else if constexpr (K == 2) return __int_as_float(FLEET_DPP(__float_as_int(x), 0x141));
+    else if constexpr (K == 3) return __int_as_float(FLEET_DPP(__float_as_int(x), 0x140));
+    else if constexpr (K == 4)
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+    else
+        return __int_as_float(__builtin_amdgcn_ds_bpermute(
+            (int)(((threadIdx.x & (kLanes - 1)) ^ 32u) << 2), __float_as_int(x)));
+}
+constexpr int kMsumDual[6] = {5, 6, 12, 8, 16, 32};
+
+template <int K, int LEN, int N>
+__device__ __forceinline__ void msum_step(float (&v)[N]) {
+    if constexpr (K < 6) {
+        if constexpr (LEN > 1) {
+            const bool up = __builtin_popcount((threadIdx.x & (kLanes - 1)) & kMsumDual[K]) & 1;
+#pragma unroll
+            for (int j = 0; j < LEN / 2; ++j) {
+                const float lo = v[j] + msum_xchg<K>(v[j]);
+                const float hi = v[j + LEN / 2] + msum_xchg<K>(v[j + LEN / 2]);
+                v[j] = up ? hi : lo;
+            }
+            msum_step<K + 1, LEN / 2, N>(v);
+        } else {
+            v[0] += msum_xchg<K>(v[0]);
+            msum_step<K + 1, 1, N>(v);
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float wave_msum(float (&v)[N]) {
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N is a power of two <= 64");
+    msum_step<0, N, N>(v);
+    return v[0];
+}
+
+template <int N>
+__device__ __forceinline__ int msum_index(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int k = 0; (1 << k) < N; ++k)
+        idx = (idx << 1) | (__builtin_popcount(lane & kMsumDual[k]) & 1);
+    return idx;
+}
+
 // Softmax over one logit per lane (lanes >= n are padding) and greedy top-k
 // with ties to the lowest index, for one whole wave, entirely in registers:
 //   z = fp32(logit + bias), m = max z, e = exp(z - m) in fp64,

@@ -155,14 +155,6 @@ __device__ __forceinline__ void item_of(int wg, int j, int& unit, int& pair) {
     }
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
-}
-// 16-byte device-scope (sc1) load: sees the latest values written by any CU.
-__device__ __forceinline__ u32x4 ld_dev16(__amdgpu_buffer_rsrc_t r, int byte_off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16);
-}
-
 // Polls the 64 exact router words (one per lane) until every tag is this
 // call's epoch; four polls in flight. Returns false if the bound ran out.
 __device__ bool poll_exact_logits(const Params& P, uint32_t epoch, float& logit) {

@@ -1,5 +1,5 @@
-// Multi-token grouped-expert MoE step (config: T tokens, each routed to 6 of
-// 64 experts, plus the shared expert on every token).
+// Multi-token grouped-expert MoE step: T tokens, each routed to 6 of 64
+// experts (ids and weights given), plus the shared expert on every token.
 //
 // The reference has no kernel for this (it is batch-1 only); the semantics are
 // HF DeepseekV2MoE.moe_infer (reference/modeling_deepseek.py:591-664): count
@@ -7,17 +7,32 @@
 // are contiguous, run each expert's SwiGLU on its rows, un-permute and combine
 // per token with the rounding of src/host/reference_decode.py:280-287.
 //
-// Four launches on the caller's stream:
-//   1. permute   - one workgroup: per-expert counts, offsets, and the stable
-//                  position of every (token, slot) entry; per-expert work tiles.
-//   2. gate/up   - every selected expert's interleaved gate/up rows in tiles
-//                  of 16 rows x up to 64 tokens: bf16 MFMA (16x16x32) when the
-//                  expert holds >= kMfmaMin tokens, a register-streamed GEMV
-//                  over the expert's few tokens below that. h is bf16.
-//   3. down      - same tiling over the 2048 down rows; the epilogue applies
-//                  bf16(w * bf16(d)) per entry (shared: bf16(d)).
-//   4. combine   - out[t] = bf16(bf16(sum_k part[t,k]) + shared[t]), k order.
-// Weights stream once per (expert, 64-token group); activations come from L2.
+// Launch shape. Work is cut into items that every workgroup takes from a
+// contiguous range holding 1/256 of the bytes, after building the dispatch
+// tables itself in LDS from the T x 6 ids (ballot-matched per-chunk counts, a
+// scan, stable positions): units = [shared expert (T tokens), then every
+// selected expert in id order (its tokens in token order)].
+//   * VALU units (<= 8 tokens): items of two gate/up row pairs (16 KB) or 2-8
+//     down rows; rows stream with 1 KB wave loads against the tokens' x / h
+//     held in LDS (dot2, one multi-value wave reduction per item), one item
+//     per wave from an LDS ticket.
+//   * MFMA units (> 8 tokens): items of 32 rows x up to 64 tokens taken by
+//     the whole workgroup: 128-element K slices of the weight rows and of the
+//     token rows go straight to LDS (global_load_lds, 1 KB per instruction,
+//     XOR-swizzled so the MFMA operand reads are conflict-free), three slices
+//     in flight, one barrier per slice; wave w runs bf16 MFMA 16x16x32 for
+//     row tile w / 4 and token tile w % 4.
+// T <= 8 (every unit is a VALU unit): ONE launch, phases G (gate/up + SwiGLU)
+//   -> D (down) -> C (combine) handing data over through self-validating words
+//   (epoch << 32 | payload, device-scope stores and loads; no grid barrier).
+// T > 8: two launches on the stream, G, then D + C; h crosses the kernel
+//   boundary as plain bf16, so the MFMA down items load it with the same
+//   global_load_lds path as the weights.
+// Partials bf16(w * bf16(d)) (shared: bf16(d)) are published per (token,
+// slot) as tagged words of two rows; phase C sums them in slot order:
+// out[t] = bf16(bf16(sum_k part[t][k]) + part[t][shared]). The last
+// workgroup to exit advances the epoch. Every wait is bounded and records
+// FLEET_MOE_ABORT_GROUP_WAIT instead of hanging.
 #include <stddef.h>
 
 #include "moe_common.h"
@@ -27,46 +42,60 @@ namespace grouped {
 
 constexpr int kMaxTokens = 256;
 constexpr int kMaxEntries = kMaxTokens * kTopK;     // 1536
-constexpr int kTileRows = 16;
-constexpr int kGroup = 64;                          // tokens per weight pass (4 MFMA tiles)
-constexpr int kGuTiles = 2 * kInter / kTileRows;    // 176 tiles of routed gate/up
-constexpr int kSgTiles = 2 * kSharedInter / kTileRows;   // 352 tiles of shared gate/up
-constexpr int kDnTiles = kHidden / kTileRows;       // 128 tiles of down rows
-constexpr int kMfmaMin = 16;                        // tokens per expert for the MFMA path
+constexpr int kMaxChunks = kMaxEntries / kLanes;    // 24 chunks of 64 entries
+constexpr int kWG = 256;
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kLanes;
-constexpr int kGrid = 256;
+constexpr int kVMax = 8;                // VALU path for units of at most 8 tokens
+constexpr int kMGroup = 64;             // tokens per MFMA pass (4 tiles of 16)
+constexpr int kUnitsMax = 1 + kRouted;
+constexpr int kSegMax = 4;
+constexpr int kSlots = kTopK + 1;       // partial slots per token: 6 routed + shared
+constexpr int kPartWords = kHidden / 2; // 1024 words of two rows per (token, slot)
+// h words per token over all units: 6 routed units of 704 + the shared 1408.
+constexpr int kHWordsPerToken = kTopK * (kInter / 2) + kSharedInter / 2;   // 5632
+// LDS staging, shared by phase G (x rows of <= 2 VALU units: 2 x 8 x 4 KB) and
+// phase D (h rows of <= 3 VALU units: shared 8 x 5,632 B + routed 8 x 2,816 B,
+// or 3 routed).
+constexpr int kStageBytes = 3 * kVMax * kInter * 2;   // 67,584
+static_assert(2 * kVMax * kHidden * 2 <= kStageBytes, "x staging fits");
+static_assert(kVMax * (kSharedInter + kInter) * 2 <= kStageBytes, "h staging fits");
+
+// MFMA items: 32 rows x 64 tokens, K in slices of 128 through LDS.
+constexpr int kMRows = 32;
+constexpr int kKs = 128;
+constexpr int kSliceA = kMRows * kKs * 2;     // 8 KB
+constexpr int kSliceB = kMGroup * kKs * 2;    // 16 KB
+constexpr int kSliceBytes = kSliceA + kSliceB;
+constexpr int kNBuf = 3;
+constexpr int kLoadsPerWave = kSliceBytes / 1024 / kWaves;   // 3 x 1 KB per wave per slice
+static_assert(kSliceBytes % (1024 * kWaves) == 0, "slice loads split over the waves");
+
+// Sticky status bit beside FLEET_MOE_ABORT_*: LDS staging overflow (the
+// partition bounds make it unreachable; checked anyway).
+constexpr uint32_t kAbortStage = 0x200u;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Workspace. Header words match the decode workspace (status at offset 8).
 struct Header {
-    uint32_t epoch, exits, abort, n_tokens;
-    uint32_t n_items_gu, n_items_dn, pad[58];
-    int32_t cnt[kRouted];        // tokens per expert
-    int32_t off[kRouted + 1];    // exclusive scan of cnt
-    int32_t gu_base[kRouted + 2];   // first gate/up item of expert e; [64] = shared
-    int32_t dn_base[kRouted + 2];
-    int32_t pad2[1];
-    int32_t ent_at[kMaxEntries]; // sorted position -> flat entry (t * 6 + k)
-    int32_t pos_of[kMaxEntries]; // flat entry -> sorted position
+    uint32_t epoch, exits, abort;
+    uint32_t pad[61];
 };
+static_assert(offsetof(Header, abort) == 8, "status word offset");
 
 struct Layout {
-    size_t header, h_routed, h_shared, part, part_shared, total;
+    size_t h, hp, part, total;
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 __host__ __device__ inline Layout layout(int max_tokens) {
     Layout L;
-    L.header = 0;
-    L.h_routed = align256(sizeof(Header));
-    L.h_shared = L.h_routed + align256((size_t)max_tokens * kTopK * kInter * 2);
-    L.part = L.h_shared + align256((size_t)max_tokens * kSharedInter * 2);
-    L.part_shared = L.part + align256((size_t)max_tokens * kTopK * kHidden * 2);
-    L.total = L.part_shared + align256((size_t)max_tokens * kHidden * 2);
+    L.h = align256(sizeof(Header));
+    L.hp = L.h + align256((size_t)(max_tokens < kVMax ? max_tokens : kVMax) * kHWordsPerToken * 8);
+    L.part = L.hp + align256((size_t)max_tokens * kHWordsPerToken * 4);
+    L.total = L.part + align256((size_t)max_tokens * kSlots * kPartWords * 8);
     return L;
 }
 
@@ -79,79 +108,84 @@ struct Params {
     const uint16_t* x;         // bf16 [T][H]
     uint16_t* out;             // bf16 [T][H]
     Header* hdr;
-    uint16_t* h_routed;        // bf16 [6T][I], sorted positions
-    uint16_t* h_shared;        // bf16 [T][SI]
-    uint16_t* part;            // bf16 [6T][H], sorted positions
-    uint16_t* part_shared;     // bf16 [T][H]
+    uint64_t* h;               // tagged h words (single launch)
+    uint32_t* hp;              // plain h words, two bf16 each (two launches)
+    uint64_t* part;            // tagged partial words [T][7][1024]
     int T;
 };
 
-__device__ __forceinline__ int groups_of(int n) { return (n + kGroup - 1) / kGroup; }
+struct Unit {
+    int expert;     // -1: shared
+    int m;          // tokens
+    int tok0;       // first sorted position of its entries (routed)
+    int h_off;      // first h word
+    int gstart;     // first G cost unit
+    int dstart;     // first D cost unit
+};
 
-// ---------------------------------------------------------------- 1. permute
-// Lane e of wave 0 scans all entries in flat order and numbers the ones routed
-// to expert e: positions are stable (flat order within an expert), which is
-// the order of a stable argsort of the flat ids (moe_infer's `argsort`).
-__global__ __launch_bounds__(kLanes) void permute_kernel(Params P) {
-    __shared__ int s_ids[kMaxEntries];
-    const int lane = threadIdx.x;
-    const int N = P.T * kTopK;
-    Header* H = P.hdr;
-    for (int i = lane; i < N; i += kLanes) s_ids[i] = min(max(P.ids[i], 0), kRouted - 1);
-    __syncthreads();
-    int c = 0;
-    for (int i = 0; i < N; ++i) c += s_ids[i] == lane;
-    // exclusive scan over the 64 lanes (Hillis-Steele with shuffles)
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < kLanes; d <<= 1) {
-        const int o = __shfl_up(incl, d, kLanes);
-        if (lane >= d) incl += o;
-    }
-    const int off = incl - c;
-    H->cnt[lane] = c;
-    H->off[lane] = off;
-    if (lane == kLanes - 1) H->off[kRouted] = incl;
-    int run = off;
-    for (int i = 0; i < N; ++i) {
-        if (s_ids[i] == lane) {
-            H->ent_at[run] = i;
-            H->pos_of[i] = run;
-            ++run;
-        }
-    }
-    // work tiles: gate/up and down items per expert, shared last
-    const int g = c > 0 ? groups_of(c) : 0;
-    int gu = g * kGuTiles, dn = g * kDnTiles;
-    int gi = gu, di = dn;
-#pragma unroll
-    for (int d = 1; d < kLanes; d <<= 1) {
-        const int o1 = __shfl_up(gi, d, kLanes);
-        const int o2 = __shfl_up(di, d, kLanes);
-        if (lane >= d) { gi += o1; di += o2; }
-    }
-    H->gu_base[lane] = gi - gu;
-    H->dn_base[lane] = di - dn;
-    if (lane == kLanes - 1) {
-        const int gs = groups_of(P.T);
-        H->gu_base[kRouted] = gi;
-        H->dn_base[kRouted] = di;
-        H->gu_base[kRouted + 1] = gi + gs * kSgTiles;
-        H->dn_base[kRouted + 1] = di + gs * kDnTiles;
-        H->n_items_gu = gi + gs * kSgTiles;
-        H->n_items_dn = di + gs * kDnTiles;
-        H->n_tokens = P.T;
+struct Seg {
+    int unit, lo, hi, base;   // items [lo, hi) of the unit; base = first ticket
+    int stage;                // LDS staging offset (bytes) or -1
+};
+
+struct Lds {
+    int16_t ent[kMaxEntries];          // sorted position -> flat entry (t * 6 + k)
+    int16_t rank[kMaxEntries];         // rank of an entry among equal ids of its chunk
+    int ccnt[kMaxChunks][kRouted];     // per-chunk counts, then per-chunk offsets
+    int cnt[kRouted];
+    int off[kRouted];
+    Unit unit[kUnitsMax];
+    Seg gseg[kSegMax];
+    Seg dseg[kSegMax];
+    int n_units, g_total, d_total;
+    int n_gseg, n_dseg, g_items, d_items;
+    int gnext, dnext;
+    float red[kWaves][kLanes];
+    union {
+        alignas(16) uint8_t stage[kStageBytes];          // VALU units: x or h rows
+        alignas(16) uint8_t mbuf[kNBuf][kSliceBytes];    // MFMA items: K slices
+    };
+};
+
+__device__ __forceinline__ bool is_v(int m) { return m <= kVMax; }
+__device__ __forceinline__ int passes_of(int m) { return (m + kMGroup - 1) / kMGroup; }
+__device__ __forceinline__ int gpairs_of(const Unit& u) { return u.expert < 0 ? kSharedInter : kInter; }
+
+// Rows per VALU down item: R rows x M tokens values stay <= 32 accumulators.
+__device__ __forceinline__ int d_rows_v(const Unit& u) {
+    return u.expert < 0 ? (u.m > 4 ? 2 : 4) : (u.m > 4 ? 4 : 8);
+}
+
+// Items and their cost (G: 16 KB units; D: 11 KB units) of a unit. MFMA items
+// run pass-minor: item i is row block i / passes, token pass i % passes.
+__device__ __forceinline__ void g_items_of(const Unit& u, int& n, int& cost) {
+    const int pairs = gpairs_of(u);
+    if (is_v(u.m)) { n = pairs / 2; cost = 1; }
+    else { n = 2 * pairs / kMRows * passes_of(u.m); cost = 8; }
+}
+__device__ __forceinline__ void d_items_of(const Unit& u, int& n, int& cost) {
+    const bool sh = u.expert < 0;
+    if (is_v(u.m)) {
+        const int R = d_rows_v(u);
+        n = kHidden / R;
+        cost = sh ? R / 2 : R / 4;
+    } else {
+        n = kHidden / kMRows * passes_of(u.m);
+        cost = sh ? 16 : 8;
     }
 }
 
-// Which expert (64 = shared) item `it` belongs to, given bases[0..65].
-__device__ __forceinline__ int find_unit(const int32_t* base, int it) {
-    int lo = 0, hi = kRouted;      // base[lo] <= it < base[hi + 1]
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (base[mid] <= it) lo = mid; else hi = mid - 1;
-    }
-    return lo;
+__device__ __forceinline__ void flag_abort(Header* hdr, uint32_t bit) {
+    __hip_atomic_fetch_or(&hdr->abort, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void st_word(uint64_t* p, uint32_t epoch, uint32_t payload) {
+    __hip_atomic_store(p, ((uint64_t)epoch << 32) | payload, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return bf16_bits(lo) | (bf16_bits(hi) << 16);
 }
 
 __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c) {
@@ -159,155 +193,663 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c)
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// One tile: rows [r0, r0 + 16) of a row-major bf16 matrix W (leading dim K)
-// times the B columns of up to 4 x 16 tokens, where token column j of tile tt
-// reads activation row act + rowidx[16 tt + j] * act_ld (K bf16 values).
-// acc[tt] receives D[i][j] with i = 4 (lane / 16) + v, j = lane % 16.
-template <int K>
-__device__ __forceinline__ void mfma_tile(const uint16_t* W, int r0, const uint16_t* act,
-                                          int act_ld, const int* rowidx, int m, f32x4 (&acc)[4]) {
+// Inclusive prefix sum over the 64 lanes (all lanes active).
+__device__ __forceinline__ int wave_incl_scan(int v) {
     const int lane = threadIdx.x & (kLanes - 1);
+#pragma unroll
+    for (int d = 1; d < kLanes; d <<= 1) {
+        const int o = __shfl_up(v, d, kLanes);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// Workgroup-local ticket, the same value in every lane.
+__device__ __forceinline__ int claim(int* ctr, int limit) {
+    int t = 0;
+    if ((threadIdx.x & (kLanes - 1)) == 0)
+        t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    t = wave_bcast(t);
+    return t < limit ? t : -1;
+}
+
+// Workgroup barrier that orders LDS only (no wait for outstanding global
+// loads, unlike __syncthreads).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void lds_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---------------------------------------------------------------- prologue
+
+// Dispatch tables and this workgroup's item ranges, all in LDS.
+__device__ void build_tables(const Params& P, Lds& L) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
+    const int T = P.T, N = T * kTopK;
+    const int nchunks = (N + kLanes - 1) / kLanes;
+    for (int i = tid; i < nchunks * kRouted; i += kThreads) (&L.ccnt[0][0])[i] = 0;
+    if (tid == 0) { L.gnext = 0; L.dnext = 0; }
+    __syncthreads();
+    // per chunk of 64 entries: lanes with equal ids by 6 ballots; the rank of
+    // an entry among them, and the count, kept by the lowest such lane
+    for (int c = wave; c < nchunks; c += kWaves) {
+        const int i = c * kLanes + lane;
+        const bool valid = i < N;
+        const int id = valid ? min(max(P.ids[i], 0), kRouted - 1) : 0;
+        unsigned long long same = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            const unsigned long long ones = __ballot(valid && ((id >> b) & 1));
+            same &= ((id >> b) & 1) ? ones : ~ones;
+        }
+        const int r = __builtin_popcountll(same & ((1ull << lane) - 1ull));
+        if (valid) {
+            L.rank[i] = (int16_t)r;
+            if (r == 0) L.ccnt[c][id] = __builtin_popcountll(same);
+        }
+    }
+    __syncthreads();
+    if (tid < kRouted) {
+        int run = 0;
+        for (int c = 0; c < nchunks; ++c) {
+            const int v = L.ccnt[c][tid];
+            L.ccnt[c][tid] = run;
+            run += v;
+        }
+        L.cnt[tid] = run;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int c = L.cnt[lane];
+        const int pr = passes_of(c);           // 0 for an unselected expert
+        const bool v = c <= kVMax;
+        // exclusive scans over the 64 experts: entry offsets, h words, costs
+        int s_off = c, s_h = c * (kInter / 2), s_g = (kInter / 2) * (c > 0 ? (v ? 1 : pr) : 0),
+            s_d = (kHidden / 4) * (c > 0 ? (v ? 1 : pr) : 0);
+        const int e_off = s_off, e_h = s_h, e_g = s_g, e_d = s_d;
+#pragma unroll
+        for (int d = 1; d < kLanes; d <<= 1) {
+            const int a = __shfl_up(s_off, d, kLanes), b = __shfl_up(s_h, d, kLanes);
+            const int g = __shfl_up(s_g, d, kLanes), q = __shfl_up(s_d, d, kLanes);
+            if (lane >= d) { s_off += a; s_h += b; s_g += g; s_d += q; }
+        }
+        L.off[lane] = s_off - e_off;
+        const unsigned long long sel = __ballot(c > 0);
+        const int vs = T <= kVMax ? 1 : passes_of(T);
+        const int g_sh = (kSharedInter / 2) * vs, d_sh = (kHidden / 2) * vs;
+        if (c > 0) {
+            const int u = 1 + __builtin_popcountll(sel & ((1ull << lane) - 1ull));
+            L.unit[u] = Unit{lane, c, s_off - e_off, T * (kSharedInter / 2) + s_h - e_h,
+                             g_sh + s_g - e_g, d_sh + s_d - e_d};
+        }
+        if (lane == kLanes - 1) {
+            L.unit[0] = Unit{-1, T, 0, 0, 0, 0};
+            L.n_units = 1 + __builtin_popcountll(sel);
+            L.g_total = g_sh + s_g;
+            L.d_total = d_sh + s_d;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < N; i += kThreads) {
+        const int id = min(max(P.ids[i], 0), kRouted - 1);
+        L.ent[L.off[id] + L.ccnt[i >> 6][id] + L.rank[i]] = (int16_t)i;
+    }
+    // this workgroup's item ranges: items whose first cost unit lies in
+    // [ceil(w C / 256), ceil((w + 1) C / 256)), over up to 65 units
+    if (wave == 0) {
+        const int wg = blockIdx.x;
+        for (int ph = 0; ph < 2; ++ph) {
+            const int C = ph == 0 ? L.g_total : L.d_total;
+            const int lo = (wg * C + kWG - 1) / kWG, hi = ((wg + 1) * C + kWG - 1) / kWG;
+            Seg* S = ph == 0 ? L.gseg : L.dseg;
+            int ns = 0, nitems = 0;
+            for (int r0 = 0; r0 < L.n_units; r0 += kLanes) {
+                const int ui = r0 + lane;
+                const bool have = ui < L.n_units;
+                int n = 0, cost = 1, start = 0;
+                if (have) {
+                    const Unit& u = L.unit[ui];
+                    if (ph == 0) { g_items_of(u, n, cost); start = u.gstart; }
+                    else { d_items_of(u, n, cost); start = u.dstart; }
+                }
+                const int a = lo - start, b = hi - start;
+                const int i0 = a <= 0 ? 0 : min(n, (a + cost - 1) / cost);
+                const int i1 = b <= 0 ? 0 : min(n, (b + cost - 1) / cost);
+                const bool seg = have && i0 < i1;
+                const unsigned long long sm = __ballot(seg);
+                const int si = ns + __builtin_popcountll(sm & ((1ull << lane) - 1ull));
+                const int items = seg ? i1 - i0 : 0;
+                const int incl = wave_incl_scan(items);
+                if (seg && si < kSegMax) S[si] = Seg{ui, i0, i1, nitems + incl - items, -1};
+                ns += __builtin_popcountll(sm);
+                nitems += __builtin_amdgcn_readlane(incl, kLanes - 1);
+            }
+            if (lane == 0) {
+                if (ns > kSegMax) flag_abort(P.hdr, kAbortStage);
+                if (ph == 0) { L.n_gseg = min(ns, kSegMax); L.g_items = nitems; }
+                else { L.n_dseg = min(ns, kSegMax); L.d_items = nitems; }
+            }
+        }
+        lds_wave_sync();
+        if (lane == 0) {
+            // LDS staging for the VALU units of each phase
+            int at = 0;
+            for (int s = 0; s < L.n_gseg; ++s) {
+                const Unit& un = L.unit[L.gseg[s].unit];
+                if (!is_v(un.m)) continue;
+                const int need = un.m * kHidden * 2;
+                if (at + need <= kStageBytes) { L.gseg[s].stage = at; at += need; }
+                else flag_abort(P.hdr, kAbortStage);
+            }
+            at = 0;
+            for (int s = 0; s < L.n_dseg; ++s) {
+                const Unit& un = L.unit[L.dseg[s].unit];
+                if (!is_v(un.m)) continue;
+                const int need = un.m * gpairs_of(un) * 2;
+                if (at + need <= kStageBytes) { L.dseg[s].stage = at; at += need; }
+                else flag_abort(P.hdr, kAbortStage);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Activation row (token) of unit position j.
+__device__ __forceinline__ int token_of(const Lds& L, const Unit& u, int j) {
+    return u.expert < 0 ? j : L.ent[u.tok0 + j] / kTopK;
+}
+
+// ---------------------------------------------------------------- phase G
+
+// VALU item: row pairs 2i, 2i+1 of a unit with m <= 8 tokens whose x rows sit
+// in LDS at `xs`. Writes h word i of every token (plain with two launches,
+// tagged with one).
+template <int M>
+__device__ __forceinline__ void g_item_v(const Params& P, Lds& L, const Unit& u, int i,
+                                         const uint8_t* xs, uint32_t epoch) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const uint16_t* blk = u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
+    const u32x4* base = reinterpret_cast<const u32x4*>(blk) + (int64_t)(2 * i) * 2 * kRowChunks;
+    u32x4 W[16];   // rows g(2i), u(2i), g(2i+1), u(2i+1): 4 chunks each
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) W[4 * r + c] = ld_stream(base + r * kRowChunks + lane + kLanes * c);
+    constexpr int NV = 4 * M;
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] = 0.f;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(xs);
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        if (j < u.m) {
+            u32x4 xq[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) xq[c] = xr[j * kRowChunks + lane + kLanes * c];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[r * M + j] = dot8_d2(W[4 * r + c], xq[c], acc[r * M + j]);
+        }
+    }
+    const float tot = wave_msum<NV>(acc);
+    const int wave = threadIdx.x >> 6;
+    float* red = L.red[wave];
+    red[msum_index<NV>(lane)] = tot;
+    lds_wave_sync();
+    if (lane < u.m) {
+        const int j = lane;
+        const float g0 = red[0 * M + j], u0 = red[1 * M + j];
+        const float g1 = red[2 * M + j], u1 = red[3 * M + j];
+        const float h0 = bf16r(bf16r(silu_rn(bf16r(g0))) * bf16r(u0));
+        const float h1 = bf16r(bf16r(silu_rn(bf16r(g1))) * bf16r(u1));
+        const int64_t w = u.h_off + (int64_t)j * (gpairs_of(u) / 2) + i;
+        if (P.hp) P.hp[w] = pack_bf16(h0, h1);
+        else st_word(P.h + w, epoch, pack_bf16(h0, h1));
+    }
+    lds_wave_sync();
+}
+
+// ---------------------------------------------------------------- MFMA items
+
+// One workgroup-cooperative MFMA item: rows [r0, r0 + 32) of A (bf16, row
+// stride lda elements) times the rows of up to 64 tokens (token j's K values
+// start at brow[j] for the loads this wave issues), K = 128 S, through LDS.
+// Slice s of the item: A rows r at [r * 256 B), B rows at 8 KB + [t * 256 B);
+// the 16-byte chunk c of row x is stored in slot c ^ (x & 15), so the 16 rows
+// an MFMA operand read touches hit 16 different slots (all 64 banks once).
+// Each wave issues 3 of the 24 1 KB loads of a slice: instruction n < 8 covers
+// A rows 4n..4n+3, n >= 8 token rows 4(n-8)..+3; lane l takes row 4n + l / 16,
+// slot l % 16. Wave w computes row tile w / 4 x token tile w % 4 (if live).
+// Returns D[4 (lane / 16) + v][lane % 16] of that tile.
+struct MItem {
+    const uint8_t* gsrc[kLoadsPerWave];   // this lane's global source for slice 0
+    int ldst[kLoadsPerWave];              // LDS offset of each of this wave's loads
+};
+
+__device__ __forceinline__ void m_issue(Lds& L, const MItem& it, int s, int buf) {
+#pragma unroll
+    for (int n = 0; n < kLoadsPerWave; ++n)
+        __builtin_amdgcn_global_load_lds(it.gsrc[n] + s * (kKs * 2), L.mbuf[buf] + it.ldst[n], 16,
+                                         0, 0);
+}
+
+__device__ __forceinline__ f32x4 m_compute(const Lds& L, int buf, bool live, f32x4 acc) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
     const int r = lane & 15, kq = lane >> 4;
-    const u32x4* wrow = reinterpret_cast<const u32x4*>(W + (int64_t)(r0 + r) * K) + kq;
-    const int nt = (m + 15) >> 4;
-    const u32x4* arow[4];
-    bool live[4];
+    const int rt = wave >> 2, tt = wave & 3;
+    if (live) {
+        const uint8_t* base = L.mbuf[buf];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-        const int j = 16 * tt + r;
-        live[tt] = j < m;
-        arow[tt] = reinterpret_cast<const u32x4*>(act + (int64_t)(live[tt] ? rowidx[j] : 0) * act_ld) + kq;
-        acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    constexpr int kSteps = K / 32;
-    constexpr int kU = (kSteps % 8 == 0) ? 8 : 4;
-    static_assert(kSteps % kU == 0, "K unroll");
-    for (int s0 = 0; s0 < kSteps; s0 += kU) {
-        u32x4 a[kU];
-#pragma unroll
-        for (int u = 0; u < kU; ++u) a[u] = ld_stream(wrow + 4 * (s0 + u));
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            if (tt < nt) {
-#pragma unroll
-                for (int u = 0; u < kU; ++u) {
-                    const u32x4 b = live[tt] ? arow[tt][4 * (s0 + u)] : u32x4{0u, 0u, 0u, 0u};
-                    acc[tt] = mfma16(a[u], b, acc[tt]);
-                }
-            }
+        for (int q = 0; q < kKs / 32; ++q) {
+            const int slot = (4 * q + kq) ^ r;
+            const u32x4 a = *reinterpret_cast<const u32x4*>(base + (16 * rt + r) * 256 + slot * 16);
+            const u32x4 b = *reinterpret_cast<const u32x4*>(base + kSliceA + (16 * tt + r) * 256 +
+                                                            slot * 16);
+            acc = mfma16(a, b, acc);
         }
     }
+    return acc;
 }
 
-// ---------------------------------------------------------------- 2. gate/up
-__global__ __launch_bounds__(kThreads) void gate_up_kernel(Params P) {
-    __shared__ int s_tok[kWaves][kGroup];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const Header* H = P.hdr;
-    const int n_items = H->n_items_gu;
-    for (int it = blockIdx.x * kWaves + wave; it < n_items; it += gridDim.x * kWaves) {
-        const int e = find_unit(H->gu_base, it);
-        const int local = it - H->gu_base[e];
-        const bool shared = e == kRouted;
-        const int tiles = shared ? kSgTiles : kGuTiles;
-        const int grp = local / tiles, tile = local - grp * tiles;
-        const int n_tok = shared ? P.T : H->cnt[e];
-        const int p0 = shared ? kGroup * grp : H->off[e] + kGroup * grp;
-        const int m = min(kGroup, n_tok - kGroup * grp);
-        // activation rows of this group: token ids in sorted order
-        if (lane < m) s_tok[wave][lane] = shared ? p0 + lane : H->ent_at[p0 + lane] / kTopK;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        const uint16_t* W = shared ? P.shared
-                                   : P.experts + (int64_t)e * P.expert_stride;
-        f32x4 acc[4];
-        mfma_tile<kHidden>(W, kTileRows * tile, P.x, kHidden, s_tok[wave], m, acc);
-        // D rows 4q+v: pair (tile*8 + 2q + v/2), v even = gate, odd = up.
-        const int q = lane >> 4, j = lane & 15;
-        const int inter = shared ? kSharedInter : kInter;
-        uint16_t* hb = shared ? P.h_shared : P.h_routed;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const int jj = 16 * tt + j;
-            if (jj < m) {
-                const int row = shared ? p0 + jj : p0 + jj;   // token (shared) or sorted position
-                const int pair = 8 * tile + 2 * q;
-                const float h0 = bf16r(bf16r(silu_rn(bf16r(acc[tt][0]))) * bf16r(acc[tt][1]));
-                const float h1 = bf16r(bf16r(silu_rn(bf16r(acc[tt][2]))) * bf16r(acc[tt][3]));
-                const uint32_t packed = bf16_bits(h0) | (bf16_bits(h1) << 16);
-                *reinterpret_cast<uint32_t*>(hb + (int64_t)row * inter + pair) = packed;
-            }
-        }
+// S slices, three in flight: at slice s a wave waits for its own loads of
+// slice s (loads return in order, so "at most the next slice's loads
+// outstanding"), the barrier makes every wave's part visible and frees the
+// buffer of slice s - 1, then slice s + 2 is issued and slice s computed.
+__device__ f32x4 m_run(Lds& L, const MItem& it, int S, bool live) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_issue(L, it, 0, 0);
+    if (S > 1) m_issue(L, it, 1, 1);
+    for (int s = 0; s < S; ++s) {
+        if (s + 1 < S) __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerWave);   // vmcnt(3)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                             // vmcnt(0)
+        lds_barrier();
+        if (s + 2 < S) m_issue(L, it, s + 2, (s + 2) % kNBuf);
+        acc = m_compute(L, s % kNBuf, live, acc);
     }
+    __syncthreads();    // the next item reuses the buffers
+    return acc;
 }
 
-// ---------------------------------------------------------------- 3. down
-__global__ __launch_bounds__(kThreads) void down_kernel(Params P) {
-    __shared__ int s_row[kWaves][kGroup];
+// Sources of this wave's loads. A: rows r0.. of `A` (stride lda elements);
+// B: token rows given by `brow(t)` (a pointer to the row's first element).
+template <typename BRow>
+__device__ __forceinline__ MItem m_setup(const uint16_t* A, int64_t lda, int r0, BRow brow) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const Header* H = P.hdr;
-    const int n_items = H->n_items_dn;
-    for (int it = blockIdx.x * kWaves + wave; it < n_items; it += gridDim.x * kWaves) {
-        const int e = find_unit(H->dn_base, it);
-        const int local = it - H->dn_base[e];
-        const bool shared = e == kRouted;
-        const int grp = local / kDnTiles, tile = local - grp * kDnTiles;
-        const int n_tok = shared ? P.T : H->cnt[e];
-        const int p0 = shared ? kGroup * grp : H->off[e] + kGroup * grp;
-        const int m = min(kGroup, n_tok - kGroup * grp);
-        if (lane < m) s_row[wave][lane] = p0 + lane;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        f32x4 acc[4];
-        if (shared) {
-            mfma_tile<kSharedInter>(P.shared + (int64_t)2 * kSharedInter * kHidden,
-                                    kTileRows * tile, P.h_shared, kSharedInter, s_row[wave], m,
-                                    acc);
+    MItem it;
+#pragma unroll
+    for (int k = 0; k < kLoadsPerWave; ++k) {
+        const int n = wave * kLoadsPerWave + k;
+        const int p = lane & 15;
+        if (n < kSliceA / 1024) {
+            const int row = 4 * n + (lane >> 4);
+            const int c = p ^ (row & 15);
+            it.gsrc[k] = reinterpret_cast<const uint8_t*>(A + (int64_t)(r0 + row) * lda) + c * 16;
+            it.ldst[k] = n * 1024;
         } else {
-            mfma_tile<kInter>(P.experts + (int64_t)e * P.expert_stride +
-                                  (int64_t)2 * kInter * kHidden,
-                              kTileRows * tile, P.h_routed, kInter, s_row[wave], m, acc);
+            const int nb = n - kSliceA / 1024;
+            const int t = 4 * nb + (lane >> 4);
+            const int c = p ^ (t & 15);
+            it.gsrc[k] = reinterpret_cast<const uint8_t*>(brow(t)) + c * 16;
+            it.ldst[k] = kSliceA + nb * 1024;
         }
-        const int q = lane >> 4, j = lane & 15;
-        const int n0 = kTileRows * tile + 4 * q;
+    }
+    return it;
+}
+
+// MFMA item of phase G: gate/up rows [32 rb, 32 rb + 32) of unit u for its
+// tokens [64 pass, 64 pass + 64); h -> plain words.
+__device__ void g_item_m(const Params& P, Lds& L, const Unit& u, int rb, int pass) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
+    const int j0 = kMGroup * pass;
+    const int m = min(kMGroup, u.m - j0);
+    const uint16_t* W = u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
+    const MItem it = m_setup(W, kHidden, kMRows * rb, [&](int t) {
+        return P.x + (int64_t)token_of(L, u, j0 + (t < m ? t : 0)) * kHidden;
+    });
+    const int tt = wave & 3, rt = wave >> 2;
+    const f32x4 acc = m_run(L, it, kHidden / kKs, 16 * tt < m);
+    // D rows 4q + v of row tile rt: pair (32 rb + 16 rt + 4q) / 2 + v / 2
+    const int q = lane >> 4, j = lane & 15;
+    const int jj = 16 * tt + j;
+    if (jj < m) {
+        const float h0 = bf16r(bf16r(silu_rn(bf16r(acc[0]))) * bf16r(acc[1]));
+        const float h1 = bf16r(bf16r(silu_rn(bf16r(acc[2]))) * bf16r(acc[3]));
+        P.hp[u.h_off + (int64_t)(j0 + jj) * (gpairs_of(u) / 2) + 8 * rb + 4 * rt + q] =
+            pack_bf16(h0, h1);
+    }
+}
+
+// ---------------------------------------------------------------- phase D
+
+// Partial words of `pos` (unit position) for rows 2w, 2w + 1: routed values
+// are bf16(w * bf16(d)), shared bf16(d).
+__device__ __forceinline__ void put_part(const Params& P, const Lds& L, const Unit& u, int pos,
+                                         int word, float d0, float d1, uint32_t epoch) {
+    int t, slot;
+    float a, b;
+    if (u.expert < 0) {
+        t = pos;
+        slot = kTopK;
+        a = bf16r(d0);
+        b = bf16r(d1);
+    } else {
+        const int e = L.ent[u.tok0 + pos];
+        t = e / kTopK;
+        slot = e - t * kTopK;
+        const float w = P.weights[e];
+        a = w * bf16r(d0);
+        b = w * bf16r(d1);
+    }
+    st_word(P.part + ((int64_t)t * kSlots + slot) * kPartWords + word, epoch, pack_bf16(a, b));
+}
+
+// VALU item: R rows of the unit's down matrix (R x M <= 32), m <= M tokens
+// whose h rows sit in LDS at `hs` (bf16 [m][I]).
+template <int M, bool SH, int R>
+__device__ __forceinline__ void d_item_v(const Params& P, Lds& L, const Unit& u, int i,
+                                         const uint8_t* hs, uint32_t epoch) {
+    constexpr int K = SH ? kSharedInter : kInter;
+    constexpr int C = K / kChunk;          // 16-byte chunks per row: 176 / 352
+    constexpr int G = (C + kLanes - 1) / kLanes;   // 3 / 6
+    static_assert(R * M <= 32 && R % 2 == 0, "item shape");
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int row0 = R * i;
+    const uint16_t* dn = SH ? P.shared + (int64_t)2 * kSharedInter * kHidden
+                            : P.experts + (int64_t)u.expert * P.expert_stride +
+                                  (int64_t)2 * kInter * kHidden;
+    const u32x4* base = reinterpret_cast<const u32x4*>(dn) + (int64_t)row0 * C;
+    u32x4 W[R * G];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const int jj = 16 * tt + j;
-            if (jj < m) {
-                const int pos = p0 + jj;
-                uint32_t b[4];
-                if (shared) {
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) b[v] = bf16_bits(acc[tt][v]);
-                } else {
-                    const float w = P.weights[H->ent_at[pos]];
+        for (int g = 0; g < G; ++g) {
+            const int c = lane + kLanes * g;
+            W[r * G + g] = c < C ? ld_stream(base + r * C + c) : u32x4{0u, 0u, 0u, 0u};
+        }
+    constexpr int NV = R * M;
+    float acc[NV];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) b[v] = bf16_bits(w * bf16r(acc[tt][v]));
-                }
-                uint16_t* dst = (shared ? P.part_shared : P.part) + (int64_t)pos * kHidden + n0;
-                *reinterpret_cast<uint2*>(dst) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+    for (int v = 0; v < NV; ++v) acc[v] = 0.f;
+    const u32x4* hr = reinterpret_cast<const u32x4*>(hs);
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        if (j < u.m) {
+            u32x4 H[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int c = lane + kLanes * g;
+                H[g] = c < C ? hr[j * C + c] : u32x4{0u, 0u, 0u, 0u};
             }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int g = 0; g < G; ++g) acc[r * M + j] = dot8_d2(W[r * G + g], H[g], acc[r * M + j]);
+        }
+    }
+    const float tot = wave_msum<NV>(acc);
+    const int wave = threadIdx.x >> 6;
+    float* red = L.red[wave];
+    red[msum_index<NV>(lane)] = tot;
+    lds_wave_sync();
+    if (lane < u.m * (R / 2)) {
+        const int j = lane / (R / 2), wp = lane - j * (R / 2);
+        put_part(P, L, u, j, row0 / 2 + wp, red[(2 * wp) * M + j], red[(2 * wp + 1) * M + j],
+                 epoch);
+    }
+    lds_wave_sync();
+}
+
+// MFMA item of phase D: down rows [32 rb, 32 rb + 32) of unit u for its
+// tokens [64 pass, 64 pass + 64), h from the plain words.
+__device__ void d_item_m(const Params& P, const Lds& L, const Unit& u, int rb, int pass,
+                         uint32_t epoch) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
+    const int j0 = kMGroup * pass;
+    const int m = min(kMGroup, u.m - j0);
+    const bool sh = u.expert < 0;
+    const int K = gpairs_of(u);
+    const uint16_t* dn = sh ? P.shared + (int64_t)2 * kSharedInter * kHidden
+                            : P.experts + (int64_t)u.expert * P.expert_stride +
+                                  (int64_t)2 * kInter * kHidden;
+    const uint16_t* hrows = reinterpret_cast<const uint16_t*>(P.hp + u.h_off);
+    const MItem it = m_setup(dn, K, kMRows * rb, [&](int t) {
+        return hrows + (int64_t)(j0 + (t < m ? t : 0)) * K;
+    });
+    const int tt = wave & 3, rt = wave >> 2;
+    const f32x4 acc = m_run(const_cast<Lds&>(L), it, K / kKs, 16 * tt < m);
+    const int q = lane >> 4, j = lane & 15;
+    const int jj = 16 * tt + j;
+    if (jj < m) {
+        const int w0 = 16 * rb + 8 * rt + 2 * q;   // rows 32 rb + 16 rt + 4q .. + 3
+        put_part(P, L, u, j0 + jj, w0, acc[0], acc[1], epoch);
+        put_part(P, L, u, j0 + jj, w0 + 1, acc[2], acc[3], epoch);
+    }
+}
+
+// h rows of a VALU unit (plain words, written by the previous launch) into
+// LDS as bf16 [m][I].
+__device__ void stage_h_plain(const Params& P, const Unit& u, uint8_t* stage) {
+    const int n = u.m * gpairs_of(u) / 8;      // 16-byte chunks
+    const u32x4* src = reinterpret_cast<const u32x4*>(P.hp + u.h_off);
+    for (int k = threadIdx.x; k < n; k += kThreads) reinterpret_cast<u32x4*>(stage)[k] = src[k];
+}
+
+// Poll the unit's h words [j0, j0 + m) x [0, K / 2) until all carry `epoch`
+// (all threads of the workgroup share the words); when `stage` is not null the
+// bf16 payloads are written there as [m][K]. Returns false on timeout.
+__device__ bool poll_h(const Params& P, const Unit& u, int j0, int m, uint8_t* stage,
+                       uint32_t epoch) {
+    const int wpt = gpairs_of(u) / 2;
+    const int n = m * wpt / 2;             // 16-byte units (two words)
+    const __amdgpu_buffer_rsrc_t rs = rsrc(P.h + u.h_off + (int64_t)j0 * wpt);
+    bool ok = true;
+    for (int k = threadIdx.x; k < n; k += kThreads) {
+        u32x4 v;
+        uint32_t it = 0;
+        for (;; ++it) {
+            v = ld_dev16(rs, 16 * k);
+            if (v.y == epoch && v.w == epoch) break;
+            if (it >= kSpinLimit ||
+                ((it & 1023) == 1023 && ld_agent(&P.hdr->abort) != 0)) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (!ok) break;
+        if (stage) reinterpret_cast<uint2*>(stage)[k] = make_uint2(v.x, v.z);
+    }
+    if (!ok) flag_abort(P.hdr, FLEET_MOE_ABORT_GROUP_WAIT);
+    return ok;
+}
+
+// ---------------------------------------------------------------- kernel
+
+__device__ __forceinline__ bool item_at(const Seg* S, int ns, int t, int& s, int& i) {
+    for (s = 0; s < ns; ++s)
+        if (t < S[s].base + (S[s].hi - S[s].lo)) {
+            i = S[s].lo + (t - S[s].base);
+            return true;
+        }
+    return false;
+}
+
+__device__ __forceinline__ void g_item_v_any(const Params& P, Lds& L, const Unit& u, int i,
+                                             const uint8_t* xs, uint32_t epoch) {
+    if (u.m == 1) g_item_v<1>(P, L, u, i, xs, epoch);
+    else if (u.m == 2) g_item_v<2>(P, L, u, i, xs, epoch);
+    else if (u.m <= 4) g_item_v<4>(P, L, u, i, xs, epoch);
+    else g_item_v<8>(P, L, u, i, xs, epoch);
+}
+
+__device__ __forceinline__ void d_item_v_any(const Params& P, Lds& L, const Unit& u, int i,
+                                             const uint8_t* hs, uint32_t epoch) {
+    if (u.expert < 0) {
+        if (u.m == 1) d_item_v<1, true, 4>(P, L, u, i, hs, epoch);
+        else if (u.m == 2) d_item_v<2, true, 4>(P, L, u, i, hs, epoch);
+        else if (u.m <= 4) d_item_v<4, true, 4>(P, L, u, i, hs, epoch);
+        else d_item_v<8, true, 2>(P, L, u, i, hs, epoch);
+    } else {
+        if (u.m == 1) d_item_v<1, false, 8>(P, L, u, i, hs, epoch);
+        else if (u.m == 2) d_item_v<2, false, 8>(P, L, u, i, hs, epoch);
+        else if (u.m <= 4) d_item_v<4, false, 8>(P, L, u, i, hs, epoch);
+        else d_item_v<8, false, 4>(P, L, u, i, hs, epoch);
+    }
+}
+
+// VALU items of a phase, one per wave from the LDS ticket (MFMA segments are
+// skipped: the whole workgroup has run them already).
+template <bool kG>
+__device__ void v_items(const Params& P, Lds& L, uint32_t epoch) {
+    const Seg* S = kG ? L.gseg : L.dseg;
+    const int ns = kG ? L.n_gseg : L.n_dseg;
+    int* next = kG ? &L.gnext : &L.dnext;
+    const int limit = kG ? L.g_items : L.d_items;
+    for (;;) {
+        const int t = claim(next, limit);
+        if (t < 0) break;
+        int s, i;
+        if (!item_at(S, ns, t, s, i)) break;
+        const Seg& sg = S[s];
+        const Unit& u = L.unit[sg.unit];
+        if (!is_v(u.m) || sg.stage < 0) continue;
+        if (kG) g_item_v_any(P, L, u, i, L.stage + sg.stage, epoch);
+        else d_item_v_any(P, L, u, i, L.stage + sg.stage, epoch);
+    }
+}
+
+// MFMA items of a phase, taken by the whole workgroup in order.
+template <bool kG>
+__device__ void m_items(const Params& P, Lds& L, uint32_t epoch) {
+    const Seg* S = kG ? L.gseg : L.dseg;
+    const int ns = kG ? L.n_gseg : L.n_dseg;
+    for (int s = 0; s < ns; ++s) {
+        const Unit& u = L.unit[S[s].unit];
+        if (is_v(u.m)) continue;
+        const int pr = passes_of(u.m);
+        for (int i = S[s].lo; i < S[s].hi; ++i) {
+            if (kG) g_item_m(P, L, u, i / pr, i % pr);
+            else d_item_m(P, L, u, i / pr, i % pr, epoch);
         }
     }
 }
 
-// ---------------------------------------------------------------- 4. combine
-__global__ __launch_bounds__(256) void combine_kernel(Params P) {
-    const Header* H = P.hdr;
-    const int t = blockIdx.x;
-    int pos[kTopK];
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) pos[k] = H->pos_of[t * kTopK + k];
-    for (int n = threadIdx.x; n < kHidden; n += blockDim.x) {
-        float y = 0.f;
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k)
-            y += __uint_as_float((uint32_t)P.part[(int64_t)pos[k] * kHidden + n] << 16);
-        const float s = __uint_as_float((uint32_t)P.part_shared[(int64_t)t * kHidden + n] << 16);
-        P.out[(int64_t)t * kHidden + n] = (uint16_t)bf16_bits(bf16r(y) + s);
+// x rows of this workgroup's VALU units of phase G into their LDS slots.
+__device__ void stage_x(const Params& P, Lds& L) {
+    for (int s = 0; s < L.n_gseg; ++s) {
+        const Seg& sg = L.gseg[s];
+        if (sg.stage < 0) continue;
+        const Unit& u = L.unit[sg.unit];
+        u32x4* dst = reinterpret_cast<u32x4*>(L.stage + sg.stage);
+        for (int k = threadIdx.x; k < u.m * kRowChunks; k += kThreads) {
+            const int j = k / kRowChunks, c = k - j * kRowChunks;
+            dst[k] = reinterpret_cast<const u32x4*>(P.x + (int64_t)token_of(L, u, j) * kHidden)[c];
+        }
     }
+}
+
+// Phase C: the 4T output words of this workgroup.
+__device__ void combine(const Params& P, uint32_t epoch) {
+    Header* hdr = P.hdr;
+    const int nw = P.T * (kPartWords / kWG);
+    const __amdgpu_buffer_rsrc_t rp = rsrc(P.part);
+    for (int k = threadIdx.x; k < nw; k += kThreads) {
+        const int g = blockIdx.x * nw + k;
+        const int t = g / kPartWords, w = g - t * kPartWords;
+        uint32_t pay[kSlots];
+        bool ready = false;
+        for (uint32_t it = 0; !ready; ++it) {
+            ready = true;
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) {
+                const int o = (((t * kSlots + s) * kPartWords) + w) * 8;
+                const uint2 v =
+                    __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, o, 0, 16));
+                pay[s] = v.x;
+                ready &= v.y == epoch;
+            }
+            if (!ready) {
+                if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&hdr->abort) != 0)) {
+                    flag_abort(hdr, FLEET_MOE_ABORT_GROUP_WAIT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+        for (int s = 0; s < kTopK; ++s) {
+            y0 += bf_lo(pay[s]);
+            y1 += bf_hi(pay[s]);
+        }
+        const float o0 = bf16r(bf16r(y0) + bf_lo(pay[kTopK]));
+        const float o1 = bf16r(bf16r(y1) + bf_hi(pay[kTopK]));
+        reinterpret_cast<uint32_t*>(P.out)[(int64_t)t * kPartWords + w] = pack_bf16(o0, o1);
+    }
+}
+
+__device__ __forceinline__ void exit_epoch(Header* hdr, uint32_t epoch) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&hdr->exits, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&hdr->epoch, epoch);
+    }
+}
+
+// T <= 8: G -> D -> C in one launch, h as tagged words.
+__global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
+    __shared__ Lds L;
+    Header* hdr = P.hdr;
+    const uint32_t epoch = ld_agent(&hdr->epoch) + 1u;
+    build_tables(P, L);
+    stage_x(P, L);
+    __syncthreads();
+    v_items<true>(P, L, epoch);
+    __syncthreads();
+    for (int s = 0; s < L.n_dseg; ++s) {
+        const Seg& sg = L.dseg[s];
+        if (sg.stage >= 0) poll_h(P, L.unit[sg.unit], 0, L.unit[sg.unit].m, L.stage + sg.stage, epoch);
+    }
+    __syncthreads();
+    v_items<false>(P, L, epoch);
+    combine(P, epoch);
+    exit_epoch(hdr, epoch);
+}
+
+// T > 8, launch 1: phase G, h as plain words.
+__global__ __launch_bounds__(kThreads, 1) void grouped_g_kernel(Params P) {
+    __shared__ Lds L;
+    build_tables(P, L);
+    m_items<true>(P, L, 0);
+    stage_x(P, L);
+    __syncthreads();
+    v_items<true>(P, L, 0);
+}
+
+// T > 8, launch 2: phases D and C.
+__global__ __launch_bounds__(kThreads, 1) void grouped_dc_kernel(Params P) {
+    __shared__ Lds L;
+    Header* hdr = P.hdr;
+    const uint32_t epoch = ld_agent(&hdr->epoch) + 1u;
+    build_tables(P, L);
+    m_items<false>(P, L, epoch);
+    for (int s = 0; s < L.n_dseg; ++s) {
+        const Seg& sg = L.dseg[s];
+        if (sg.stage >= 0) stage_h_plain(P, L.unit[sg.unit], L.stage + sg.stage);
+    }
+    __syncthreads();
+    v_items<false>(P, L, epoch);
+    combine(P, epoch);
+    exit_epoch(hdr, epoch);
 }
 
 }  // namespace grouped
@@ -321,7 +863,7 @@ int fleet_moe_check_device(int min_cus);
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 extern "C" size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, int32_t max_tokens) {
-    (void)dims;
+    if (fleet_moe_check_dims(dims) != 0) return 0;
     if (max_tokens < 1 || max_tokens > grouped::kMaxTokens) return 0;
     return grouped::layout(max_tokens).total;
 }
@@ -346,7 +888,7 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
     for (int t = grouped::kMaxTokens; t >= 1; --t)
         if (grouped::layout(t).total <= workspace_bytes) { max_tokens = t; break; }
     if (max_tokens < n_tokens) return FLEET_MOE_ERR_WORKSPACE;
-    if (int e = fleet_moe_check_device(1)) return e;
+    if (int e = fleet_moe_check_device(grouped::kWG)) return e;
 
     const grouped::Layout L = grouped::layout(max_tokens);
     char* ws = static_cast<char*>(workspace);
@@ -358,17 +900,20 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
     P.weights = weights;
     P.x = x_norm;
     P.out = out;
-    P.hdr = reinterpret_cast<grouped::Header*>(ws + L.header);
-    P.h_routed = reinterpret_cast<uint16_t*>(ws + L.h_routed);
-    P.h_shared = reinterpret_cast<uint16_t*>(ws + L.h_shared);
-    P.part = reinterpret_cast<uint16_t*>(ws + L.part);
-    P.part_shared = reinterpret_cast<uint16_t*>(ws + L.part_shared);
+    P.hdr = reinterpret_cast<grouped::Header*>(ws);
+    P.h = reinterpret_cast<uint64_t*>(ws + L.h);
+    P.part = reinterpret_cast<uint64_t*>(ws + L.part);
     P.T = n_tokens;
-    hipLaunchKernelGGL(grouped::permute_kernel, dim3(1), dim3(kLanes), 0, stream, P);
-    hipLaunchKernelGGL(grouped::gate_up_kernel, dim3(grouped::kGrid), dim3(grouped::kThreads), 0,
-                       stream, P);
-    hipLaunchKernelGGL(grouped::down_kernel, dim3(grouped::kGrid), dim3(grouped::kThreads), 0,
-                       stream, P);
-    hipLaunchKernelGGL(grouped::combine_kernel, dim3(n_tokens), dim3(256), 0, stream, P);
+    if (n_tokens <= grouped::kVMax) {
+        P.hp = nullptr;
+        hipLaunchKernelGGL(grouped::grouped_fused_kernel, dim3(grouped::kWG),
+                           dim3(grouped::kThreads), 0, stream, P);
+    } else {
+        P.hp = reinterpret_cast<uint32_t*>(ws + L.hp);
+        hipLaunchKernelGGL(grouped::grouped_g_kernel, dim3(grouped::kWG), dim3(grouped::kThreads),
+                           0, stream, P);
+        hipLaunchKernelGGL(grouped::grouped_dc_kernel, dim3(grouped::kWG),
+                           dim3(grouped::kThreads), 0, stream, P);
+    }
     return (int)hipGetLastError();
 }

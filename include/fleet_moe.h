@@ -101,14 +101,17 @@ size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, int32_t max
 
 /* Multi-token grouped-expert product for one layer (no reference kernel; HF
  * DeepseekV2MoE.forward + moe_infer, reference/modeling_deepseek.py:568-664):
- * tokens are permuted by expert, every selected expert runs its SwiGLU over
- * its token rows (bf16 MFMA where an expert holds >= 16 tokens, GEMV below),
- * and out[t] = bf16(bf16(sum_k bf16(w[t][k] * E_{ids[t][k]}(x[t]))) +
+ * tokens are grouped by expert, every selected expert runs its SwiGLU over
+ * its tokens (VALU GEMV for an expert holding <= 8 tokens, bf16 MFMA above
+ * that), and out[t] = bf16(bf16(sum_k bf16(w[t][k] * E_{ids[t][k]}(x[t]))) +
  * shared(x[t])), the per-token combine of src/host/reference_decode.py:
- * 280-287, so grouped(T) equals T batch-1 MoE outputs.
+ * 280-287, so grouped(T) equals T batch-1 MoE outputs up to fp32 summation
+ * order. One launch over every CU (256 workgroups resident at once).
  * x_norm: bf16[n_tokens][hidden]; ids: int32[n_tokens][top_k] (each in
  * [0, n_routed), distinct per token); weights: fp32[n_tokens][top_k];
- * out: bf16[n_tokens][hidden]. 1 <= n_tokens <= max_tokens of the workspace. */
+ * out: bf16[n_tokens][hidden]. 1 <= n_tokens <= max_tokens of the workspace
+ * (max_tokens <= 256). Workspace words carry a 32-bit call count: a
+ * workspace is good for 2^32 calls. */
 int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens, const int32_t* ids,
                       const float* weights, const uint16_t* x_norm, uint16_t* out,
                       void* workspace, size_t workspace_bytes, const fleet_moe_dims* dims,

@@ -100,3 +100,23 @@ def test_grouped_hot_expert_over_64_tokens(dev):
     got = ops.bf16_bits_to_f32(out).cpu().numpy()
     want = orc.moe_grouped(pl, xn, ids, ws)["out"]
     assert rel_err(got, want) <= 1e-2
+
+
+def test_grouped_workspace_reuse_across_token_counts(dev):
+    """One workspace, calls of T = 64, 4, 16, 1, 64 in a row: words left by a
+    larger earlier call are never taken for the current call's (each call's
+    words carry its own call count), so every result matches the oracle."""
+    layer, pl = dev
+    runner = ops.GroupedRunner(64, DSV2_LITE)
+    bias = synth.zipf_logit_bias(1)
+    for n, T in enumerate((64, 4, 16, 1, 64)):
+        xn = orc.rms_norm(synth.hidden_inputs(70 + n, T))
+        _, ids, ws = orc.route(pl.router_f32(), xn, logit_bias=bias)
+        say(f"grouped reuse call {n} T={T}")
+        out = runner.run(layer, torch.from_numpy(orc.bf16_bits(xn).view(np.int16)).cuda(),
+                         torch.from_numpy(ids).cuda(), torch.from_numpy(ws).cuda())
+        torch.cuda.synchronize()
+        got = ops.bf16_bits_to_f32(out).cpu().numpy()
+        want = orc.moe_grouped(pl, xn, ids, ws)["out"]
+        assert rel_err(got, want) <= 1e-2, f"call {n} T={T}"
+    assert runner.status() == 0
