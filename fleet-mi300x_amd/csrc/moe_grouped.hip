@@ -61,14 +61,16 @@ constexpr int kStageBytes = 3 * kVMax * kInter * 2;   // 67,584
 static_assert(2 * kVMax * kHidden * 2 <= kStageBytes, "x staging fits");
 static_assert(kVMax * (kSharedInter + kInter) * 2 <= kStageBytes, "h staging fits");
 
-// MFMA items: 32 rows x 64 tokens, K in slices of 128 through LDS.
+// MFMA items: 32 rows x 64 tokens, K in slices of 256 (512 B of every row)
+// through LDS; a K of 1408 ends with a half slice.
 constexpr int kMRows = 32;
-constexpr int kKs = 128;
-constexpr int kSliceA = kMRows * kKs * 2;     // 8 KB
-constexpr int kSliceB = kMGroup * kKs * 2;    // 16 KB
-constexpr int kSliceBytes = kSliceA + kSliceB;
-constexpr int kNBuf = 3;
-constexpr int kLoadsPerWave = kSliceBytes / 1024 / kWaves;   // 3 x 1 KB per wave per slice
+constexpr int kKs = 256;
+constexpr int kRowSlice = kKs * 2;                 // 512 B
+constexpr int kSliceA = kMRows * kRowSlice;        // 16 KB
+constexpr int kSliceB = kMGroup * kRowSlice;       // 32 KB
+constexpr int kSliceBytes = kSliceA + kSliceB;     // 48 KB
+constexpr int kNBuf = 3;                           // two slices in flight
+constexpr int kLoadsPerWave = kSliceBytes / 1024 / kWaves;   // 6 x 1 KB per wave per slice
 static_assert(kSliceBytes % (1024 * kWaves) == 0, "slice loads split over the waves");
 
 // Sticky status bit beside FLEET_MOE_ABORT_*: LDS staging overflow (the
@@ -130,8 +132,6 @@ struct Seg {
 
 struct Lds {
     int16_t ent[kMaxEntries];          // sorted position -> flat entry (t * 6 + k)
-    int16_t rank[kMaxEntries];         // rank of an entry among equal ids of its chunk
-    int ccnt[kMaxChunks][kRouted];     // per-chunk counts, then per-chunk offsets
     int cnt[kRouted];
     int off[kRouted];
     Unit unit[kUnitsMax];
@@ -144,6 +144,11 @@ struct Lds {
     union {
         alignas(16) uint8_t stage[kStageBytes];          // VALU units: x or h rows
         alignas(16) uint8_t mbuf[kNBuf][kSliceBytes];    // MFMA items: K slices
+        struct {                                         // prologue only
+            int8_t id[kMaxEntries];      // ids, clamped to [0, 64)
+            int16_t rank[kMaxEntries];   // rank of an entry among equal ids of its chunk
+            int ccnt[kMaxChunks][kRouted];   // per-chunk counts, then per-chunk offsets
+        } pro;
     };
 };
 
@@ -193,14 +198,16 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c)
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Inclusive prefix sum over the 64 lanes (all lanes active).
+// Inclusive prefix sum over the 64 lanes (all lanes active), DPP only:
+// row_shr 1, 2, 4, 8 within each row of 16 (lanes without a source add 0),
+// then row_bcast 15 into rows 1 and 3 and row_bcast 31 into rows 2 and 3.
 __device__ __forceinline__ int wave_incl_scan(int v) {
-    const int lane = threadIdx.x & (kLanes - 1);
-#pragma unroll
-    for (int d = 1; d < kLanes; d <<= 1) {
-        const int o = __shfl_up(v, d, kLanes);
-        if (lane >= d) v += o;
-    }
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
     return v;
 }
 
@@ -234,7 +241,7 @@ __device__ void build_tables(const Params& P, Lds& L) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
     const int T = P.T, N = T * kTopK;
     const int nchunks = (N + kLanes - 1) / kLanes;
-    for (int i = tid; i < nchunks * kRouted; i += kThreads) (&L.ccnt[0][0])[i] = 0;
+    for (int i = tid; i < nchunks * kRouted; i += kThreads) (&L.pro.ccnt[0][0])[i] = 0;
     if (tid == 0) { L.gnext = 0; L.dnext = 0; }
     __syncthreads();
     // per chunk of 64 entries: lanes with equal ids by 6 ballots; the rank of
@@ -243,6 +250,7 @@ __device__ void build_tables(const Params& P, Lds& L) {
         const int i = c * kLanes + lane;
         const bool valid = i < N;
         const int id = valid ? min(max(P.ids[i], 0), kRouted - 1) : 0;
+        if (valid) L.pro.id[i] = (int8_t)id;
         unsigned long long same = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 6; ++b) {
@@ -251,16 +259,16 @@ __device__ void build_tables(const Params& P, Lds& L) {
         }
         const int r = __builtin_popcountll(same & ((1ull << lane) - 1ull));
         if (valid) {
-            L.rank[i] = (int16_t)r;
-            if (r == 0) L.ccnt[c][id] = __builtin_popcountll(same);
+            L.pro.rank[i] = (int16_t)r;
+            if (r == 0) L.pro.ccnt[c][id] = __builtin_popcountll(same);
         }
     }
     __syncthreads();
     if (tid < kRouted) {
         int run = 0;
         for (int c = 0; c < nchunks; ++c) {
-            const int v = L.ccnt[c][tid];
-            L.ccnt[c][tid] = run;
+            const int v = L.pro.ccnt[c][tid];
+            L.pro.ccnt[c][tid] = run;
             run += v;
         }
         L.cnt[tid] = run;
@@ -274,12 +282,10 @@ __device__ void build_tables(const Params& P, Lds& L) {
         int s_off = c, s_h = c * (kInter / 2), s_g = (kInter / 2) * (c > 0 ? (v ? 1 : pr) : 0),
             s_d = (kHidden / 4) * (c > 0 ? (v ? 1 : pr) : 0);
         const int e_off = s_off, e_h = s_h, e_g = s_g, e_d = s_d;
-#pragma unroll
-        for (int d = 1; d < kLanes; d <<= 1) {
-            const int a = __shfl_up(s_off, d, kLanes), b = __shfl_up(s_h, d, kLanes);
-            const int g = __shfl_up(s_g, d, kLanes), q = __shfl_up(s_d, d, kLanes);
-            if (lane >= d) { s_off += a; s_h += b; s_g += g; s_d += q; }
-        }
+        s_off = wave_incl_scan(s_off);
+        s_h = wave_incl_scan(s_h);
+        s_g = wave_incl_scan(s_g);
+        s_d = wave_incl_scan(s_d);
         L.off[lane] = s_off - e_off;
         const unsigned long long sel = __ballot(c > 0);
         const int vs = T <= kVMax ? 1 : passes_of(T);
@@ -298,8 +304,8 @@ __device__ void build_tables(const Params& P, Lds& L) {
     }
     __syncthreads();
     for (int i = tid; i < N; i += kThreads) {
-        const int id = min(max(P.ids[i], 0), kRouted - 1);
-        L.ent[L.off[id] + L.ccnt[i >> 6][id] + L.rank[i]] = (int16_t)i;
+        const int id = L.pro.id[i];
+        L.ent[L.off[id] + L.pro.ccnt[i >> 6][id] + L.pro.rank[i]] = (int16_t)i;
     }
     // this workgroup's item ranges: items whose first cost unit lies in
     // [ceil(w C / 256), ceil((w + 1) C / 256)), over up to 65 units
@@ -420,59 +426,84 @@ __device__ __forceinline__ void g_item_v(const Params& P, Lds& L, const Unit& u,
 // ---------------------------------------------------------------- MFMA items
 
 // One workgroup-cooperative MFMA item: rows [r0, r0 + 32) of A (bf16, row
-// stride lda elements) times the rows of up to 64 tokens (token j's K values
-// start at brow[j] for the loads this wave issues), K = 128 S, through LDS.
-// Slice s of the item: A rows r at [r * 256 B), B rows at 8 KB + [t * 256 B);
-// the 16-byte chunk c of row x is stored in slot c ^ (x & 15), so the 16 rows
-// an MFMA operand read touches hit 16 different slots (all 64 banks once).
-// Each wave issues 3 of the 24 1 KB loads of a slice: instruction n < 8 covers
-// A rows 4n..4n+3, n >= 8 token rows 4(n-8)..+3; lane l takes row 4n + l / 16,
-// slot l % 16. Wave w computes row tile w / 4 x token tile w % 4 (if live).
-// Returns D[4 (lane / 16) + v][lane % 16] of that tile.
+// stride lda elements) times the rows of up to 64 tokens, K = 256 S (+ 128 for
+// a half tail slice), through LDS. Slice s: A row r at [r * 512 B), token row
+// t at 16 KB + [t * 512 B); the 16-byte chunk c of row x sits in slot
+// c ^ (x & 15), so the 16 rows an MFMA operand read touches hit 16 different
+// slots (all 64 banks once). A slice takes 16 + 8 nt 1 KB loads (nt live
+// token tiles): load n < 16 covers A rows 2n, 2n + 1, load n >= 16 token rows
+// 2(n-16), +1; lane l takes row 2n + l / 32, slot l % 32. Wave w issues the
+// contiguous block of loads [w p, w p + p), p = ceil(total / 8) <= 6. Wave w
+// computes row tile w / 4 x token tile w % 4
+// (if live) and returns D[4 (lane / 16) + v][lane % 16].
 struct MItem {
-    const uint8_t* gsrc[kLoadsPerWave];   // this lane's global source for slice 0
+    const uint8_t* gsrc[kLoadsPerWave];   // this lane's global source, full slices
+    const uint8_t* gtail[kLoadsPerWave];  // same for a half slice (chunks 0..15 only)
     int ldst[kLoadsPerWave];              // LDS offset of each of this wave's loads
+    int mine;                             // loads this wave issues per slice
 };
 
-__device__ __forceinline__ void m_issue(Lds& L, const MItem& it, int s, int buf) {
+__device__ __forceinline__ void m_issue(Lds& L, const MItem& it, int s, int buf, bool tail) {
 #pragma unroll
     for (int n = 0; n < kLoadsPerWave; ++n)
-        __builtin_amdgcn_global_load_lds(it.gsrc[n] + s * (kKs * 2), L.mbuf[buf] + it.ldst[n], 16,
-                                         0, 0);
+        if (n < it.mine)
+            __builtin_amdgcn_global_load_lds((tail ? it.gtail[n] : it.gsrc[n]) + s * kRowSlice,
+                                             L.mbuf[buf] + it.ldst[n], 16, 0, 0);
 }
 
-__device__ __forceinline__ f32x4 m_compute(const Lds& L, int buf, bool live, f32x4 acc) {
+// All operands of the slice are read before its MFMAs (the waves run in step
+// between barriers and cannot hide each other's LDS latency).
+template <int Q>
+__device__ __forceinline__ f32x4 m_compute(const Lds& L, int buf, f32x4 acc) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
     const int r = lane & 15, kq = lane >> 4;
     const int rt = wave >> 2, tt = wave & 3;
-    if (live) {
-        const uint8_t* base = L.mbuf[buf];
+    const uint8_t* base = L.mbuf[buf];
+    u32x4 a[Q], b[Q];
 #pragma unroll
-        for (int q = 0; q < kKs / 32; ++q) {
-            const int slot = (4 * q + kq) ^ r;
-            const u32x4 a = *reinterpret_cast<const u32x4*>(base + (16 * rt + r) * 256 + slot * 16);
-            const u32x4 b = *reinterpret_cast<const u32x4*>(base + kSliceA + (16 * tt + r) * 256 +
-                                                            slot * 16);
-            acc = mfma16(a, b, acc);
-        }
+    for (int q = 0; q < Q; ++q) {
+        const int slot = (4 * q + kq) ^ r;
+        a[q] = *reinterpret_cast<const u32x4*>(base + (16 * rt + r) * kRowSlice + slot * 16);
+        b[q] = *reinterpret_cast<const u32x4*>(base + kSliceA + (16 * tt + r) * kRowSlice +
+                                                slot * 16);
     }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) acc = mfma16(a[q], b[q], acc);
     return acc;
 }
 
-// S slices, three in flight: at slice s a wave waits for its own loads of
-// slice s (loads return in order, so "at most the next slice's loads
-// outstanding"), the barrier makes every wave's part visible and frees the
-// buffer of slice s - 1, then slice s + 2 is issued and slice s computed.
-__device__ f32x4 m_run(Lds& L, const MItem& it, int S, bool live) {
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 6].
+__device__ __forceinline__ void wait_loads_except(int n) {
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+        case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    }
+}
+
+// S slices (the last one half when `tail`), two in flight: at slice s a wave
+// waits for its own loads of slice s (loads return in order, so "only the next
+// slice's loads outstanding"), the barrier makes every wave's part visible and
+// frees the buffer of slice s - 1, then slice s + 2 is issued into it and
+// slice s computed. The barrier orders LDS only: it does not wait for the
+// loads in flight.
+__device__ f32x4 m_run(Lds& L, const MItem& it, int S, bool tail, bool live) {
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_issue(L, it, 0, 0);
-    if (S > 1) m_issue(L, it, 1, 1);
+    m_issue(L, it, 0, 0, tail && S == 1);
+    if (S > 1) m_issue(L, it, 1, 1, tail && S == 2);
     for (int s = 0; s < S; ++s) {
-        if (s + 1 < S) __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerWave);   // vmcnt(3)
-        else __builtin_amdgcn_s_waitcnt(0x0F70);                             // vmcnt(0)
+        if (s + 1 < S) wait_loads_except(it.mine);   // the next slice's may stay in flight
+        else __builtin_amdgcn_s_waitcnt(0x0F70);     // vmcnt(0)
         lds_barrier();
-        if (s + 2 < S) m_issue(L, it, s + 2, (s + 2) % kNBuf);
-        acc = m_compute(L, s % kNBuf, live, acc);
+        if (s + 2 < S) m_issue(L, it, s + 2, (s + 2) % kNBuf, tail && s + 3 == S);
+        if (live) {
+            if (tail && s + 1 == S) acc = m_compute<kKs / 64>(L, s % kNBuf, acc);
+            else acc = m_compute<kKs / 32>(L, s % kNBuf, acc);
+        }
     }
     __syncthreads();    // the next item reuses the buffers
     return acc;
@@ -481,25 +512,33 @@ __device__ f32x4 m_run(Lds& L, const MItem& it, int S, bool live) {
 // Sources of this wave's loads. A: rows r0.. of `A` (stride lda elements);
 // B: token rows given by `brow(t)` (a pointer to the row's first element).
 template <typename BRow>
-__device__ __forceinline__ MItem m_setup(const uint16_t* A, int64_t lda, int r0, BRow brow) {
+__device__ __forceinline__ MItem m_setup(const uint16_t* A, int64_t lda, int r0, int nt,
+                                         BRow brow) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
+    const int total = kSliceA / 1024 + 8 * nt;
+    const int per = (total + kWaves - 1) / kWaves;
     MItem it;
+    it.mine = wave_bcast(max(0, min(per, total - wave * per)));   // wave-uniform (SGPR)
 #pragma unroll
     for (int k = 0; k < kLoadsPerWave; ++k) {
-        const int n = wave * kLoadsPerWave + k;
-        const int p = lane & 15;
+        const int n = min(wave * per + k, total - 1);   // loads past `mine` are not issued
+        const int p = lane & 31, half = lane >> 5;
+        const uint8_t* row;
+        int key;
         if (n < kSliceA / 1024) {
-            const int row = 4 * n + (lane >> 4);
-            const int c = p ^ (row & 15);
-            it.gsrc[k] = reinterpret_cast<const uint8_t*>(A + (int64_t)(r0 + row) * lda) + c * 16;
+            const int x = 2 * n + half;
+            row = reinterpret_cast<const uint8_t*>(A + (int64_t)(r0 + x) * lda);
+            key = x & 15;
             it.ldst[k] = n * 1024;
         } else {
             const int nb = n - kSliceA / 1024;
-            const int t = 4 * nb + (lane >> 4);
-            const int c = p ^ (t & 15);
-            it.gsrc[k] = reinterpret_cast<const uint8_t*>(brow(t)) + c * 16;
+            const int t = 2 * nb + half;
+            row = reinterpret_cast<const uint8_t*>(brow(t));
+            key = t & 15;
             it.ldst[k] = kSliceA + nb * 1024;
         }
+        it.gsrc[k] = row + (p ^ key) * 16;
+        it.gtail[k] = row + ((p & 15) ^ key) * 16;
     }
     return it;
 }
@@ -511,11 +550,11 @@ __device__ void g_item_m(const Params& P, Lds& L, const Unit& u, int rb, int pas
     const int j0 = kMGroup * pass;
     const int m = min(kMGroup, u.m - j0);
     const uint16_t* W = u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
-    const MItem it = m_setup(W, kHidden, kMRows * rb, [&](int t) {
+    const MItem it = m_setup(W, kHidden, kMRows * rb, (m + 15) >> 4, [&](int t) {
         return P.x + (int64_t)token_of(L, u, j0 + (t < m ? t : 0)) * kHidden;
     });
     const int tt = wave & 3, rt = wave >> 2;
-    const f32x4 acc = m_run(L, it, kHidden / kKs, 16 * tt < m);
+    const f32x4 acc = m_run(L, it, kHidden / kKs, false, 16 * tt < m);
     // D rows 4q + v of row tile rt: pair (32 rb + 16 rt + 4q) / 2 + v / 2
     const int q = lane >> 4, j = lane & 15;
     const int jj = 16 * tt + j;
@@ -620,11 +659,13 @@ __device__ void d_item_m(const Params& P, const Lds& L, const Unit& u, int rb, i
                             : P.experts + (int64_t)u.expert * P.expert_stride +
                                   (int64_t)2 * kInter * kHidden;
     const uint16_t* hrows = reinterpret_cast<const uint16_t*>(P.hp + u.h_off);
-    const MItem it = m_setup(dn, K, kMRows * rb, [&](int t) {
+    const MItem it = m_setup(dn, K, kMRows * rb, (m + 15) >> 4, [&](int t) {
         return hrows + (int64_t)(j0 + (t < m ? t : 0)) * K;
     });
     const int tt = wave & 3, rt = wave >> 2;
-    const f32x4 acc = m_run(const_cast<Lds&>(L), it, K / kKs, 16 * tt < m);
+    // K = 1408: five full slices and a half one; K = 2816: eleven full
+    const bool tail = (K % kKs) != 0;
+    const f32x4 acc = m_run(const_cast<Lds&>(L), it, K / kKs + (tail ? 1 : 0), tail, 16 * tt < m);
     const int q = lane >> 4, j = lane & 15;
     const int jj = 16 * tt + j;
     if (jj < m) {
