@@ -1,0 +1,339 @@
+"""Task-descriptor adapter: route a task graph's MoE layers to this library.
+
+The reference decode runs one persistent kernel over a list of 64-byte task
+descriptors (src/host/taskgraph.py:64-68 packs them; src/runtime/
+fleet_runtime.h:87-107 is the device struct). A MoE layer is three task kinds
+in that list (taskgraph.py:366-441):
+
+  NORM_ROUTER (4)      one per XCD: post-attention RMSNorm + router logits
+  EXPERT_GATE_UP (5)   one per XCD, `expert_slot` 0..top_k-1 (routed slot) or
+                       -1 / -2 (the two halves of the shared expert)
+  EXPERT_DOWN (6)      the same slots; all of them signal one GLOBAL event
+
+and the consumer of that event (the next layer's first tasks, or LM_HEAD)
+carries FOLD_PARTIALS: its prologue adds the eight expert partials to the
+residual stream.
+
+`plan()` reads such a list (and the `.events.txt` sidecar, when given) and cuts
+it into graph segments around every MoE layer: each MoE layer becomes one
+`fleet_moe_layer_decode` call, which does the norm, routing, experts, combine
+and residual add in one launch. Waits on events produced before a cut are
+satisfied by stream order and cleared, and FOLD_PARTIALS is cleared on the
+consumers (the residual is already final). Every MoE layer must be complete
+(a router task on every XCD, gate_up and down for every routed slot and both
+shared halves) or `plan()` raises.
+
+`MoeSteps.run()` executes the MoE calls of a plan on this library; the graph
+segments are left to the runtime that owns them.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass, field, replace
+from enum import IntEnum, IntFlag
+
+DESCRIPTOR_BYTES = 64
+# Field order and widths of struct TaskDescriptor (fleet_runtime.h:87-107):
+# kind u16, fifteen i16, index i32, 28 bytes of padding, little-endian.
+_FORMAT = "<H15hi28x"
+assert struct.calcsize(_FORMAT) == DESCRIPTOR_BYTES
+FIELD_NAMES = ("kind", "layer", "xcd", "worker", "wait_event", "signal_event",
+               "signal_scope", "n_split", "head", "kv_chunk", "expert_slot",
+               "wait_scope", "wait_count", "local_event", "flags",
+               "signal_xcd_count", "index")
+N_XCDS = 8
+
+
+class TaskKind(IntEnum):
+    """Task kinds (taskgraph.py:73-88); the MoE path is 4, 5 and 6."""
+    QKV_FUSED = 0
+    ATTENTION = 1
+    MERGE_UV = 2
+    O_PROJ = 3
+    NORM_ROUTER = 4
+    EXPERT_GATE_UP = 5
+    EXPERT_DOWN = 6
+    REDUCE = 7
+    DENSE_GATE_UP = 8
+    DENSE_DOWN = 9
+    EMBED = 10
+    LM_HEAD = 11
+    ARGMAX = 12
+    PREFETCH = 13
+    Q_ABSORB = 14
+
+
+class Flags(IntFlag):
+    """Descriptor flag bits (taskgraph.py:91-126, fleet_runtime.h TaskFlags)."""
+    NONE = 0
+    FOLD_PARTIALS = 1
+    SIGNAL_LAST = 2
+    CHUNK_SIGNAL = 8
+    CHUNK_WAIT = 16
+    KVA_SHARED = 32
+    WORKER_GROUP = 64
+    ROUTING_CACHED = 128
+    TOPK_PUBLISH = 256
+    TOPK_READ = 512
+    PUB_WAIT = 1024
+    OPROJ_ROW_SPLIT = 2048
+    LOCAL_FOLD = 4096
+    LOCAL_KVA = 8192
+
+
+class Scope(IntEnum):
+    """Event scope (taskgraph.py:147-151)."""
+    NONE = 0
+    XCD_LOCAL = 1
+    GLOBAL = 2
+
+
+MOE_KINDS = (TaskKind.NORM_ROUTER, TaskKind.EXPERT_GATE_UP, TaskKind.EXPERT_DOWN)
+
+
+@dataclass(frozen=True)
+class Descriptor:
+    """One 64-byte task descriptor; -1 means "none" for event fields."""
+    kind: int
+    layer: int = -1
+    xcd: int = -1
+    worker: int = -1
+    wait_event: int = -1
+    signal_event: int = -1
+    signal_scope: int = 0
+    n_split: int = 1
+    head: int = -1
+    kv_chunk: int = -1
+    expert_slot: int = -1
+    wait_scope: int = 0
+    wait_count: int = 0
+    local_event: int = -1
+    flags: int = 0
+    signal_xcd_count: int = 0
+    index: int = -1
+
+    def pack(self) -> bytes:
+        return struct.pack(_FORMAT, *(getattr(self, n) for n in FIELD_NAMES))
+
+    @classmethod
+    def unpack(cls, b: bytes) -> "Descriptor":
+        return cls(*struct.unpack(_FORMAT, b))
+
+
+def pack_all(descs) -> bytes:
+    return b"".join(d.pack() for d in descs)
+
+
+def unpack_all(buf: bytes) -> list[Descriptor]:
+    if len(buf) % DESCRIPTOR_BYTES:
+        raise ValueError(f"descriptor stream of {len(buf)} bytes is not a multiple of "
+                         f"{DESCRIPTOR_BYTES}")
+    return [Descriptor.unpack(buf[o:o + DESCRIPTOR_BYTES])
+            for o in range(0, len(buf), DESCRIPTOR_BYTES)]
+
+
+@dataclass(frozen=True)
+class Event:
+    id: int
+    scope: int
+    producers: int
+    label: str
+
+
+def parse_events(text: str) -> list[Event]:
+    """The `.events.txt` sidecar: one `id scope producers label` per line
+    (taskgraph.py:835-837)."""
+    out = []
+    for ln, line in enumerate(text.splitlines(), 1):
+        if not line.strip():
+            continue
+        parts = line.split(maxsplit=3)
+        if len(parts) < 3:
+            raise ValueError(f"events line {ln}: expected `id scope producers label`")
+        out.append(Event(int(parts[0]), int(parts[1]), int(parts[2]),
+                         parts[3] if len(parts) > 3 else ""))
+    return out
+
+
+@dataclass
+class MoeLayer:
+    """The MoE tasks of one layer, as found in the graph."""
+    layer: int
+    routers: list[Descriptor] = field(default_factory=list)
+    gate_up: list[Descriptor] = field(default_factory=list)
+    down: list[Descriptor] = field(default_factory=list)
+
+    @property
+    def done_event(self) -> int:
+        ev = {d.signal_event for d in self.down}
+        if len(ev) != 1:
+            raise ValueError(f"layer {self.layer}: expert down tasks signal {sorted(ev)}, "
+                             "expected one event")
+        return ev.pop()
+
+    def check(self, top_k: int, n_xcds: int = N_XCDS) -> None:
+        want = set(range(top_k)) | {-1, -2}
+        if {d.xcd for d in self.routers} != set(range(n_xcds)):
+            raise ValueError(f"layer {self.layer}: NORM_ROUTER tasks on XCDs "
+                             f"{sorted({d.xcd for d in self.routers})}, expected all {n_xcds}")
+        for name, group in (("EXPERT_GATE_UP", self.gate_up), ("EXPERT_DOWN", self.down)):
+            got = {d.expert_slot for d in group}
+            if got != want:
+                raise ValueError(f"layer {self.layer}: {name} slots {sorted(got)}, "
+                                 f"expected {sorted(want)}")
+        _ = self.done_event
+
+
+@dataclass
+class Segment:
+    """Graph descriptors to run as one launch of the owning runtime."""
+    descriptors: list[Descriptor]
+
+
+@dataclass
+class MoeCall:
+    """One fleet_moe_layer_decode call replacing a MoE layer's tasks."""
+    layer: int
+    source: MoeLayer
+
+
+def _moe_layers(descs: list[Descriptor]) -> dict[int, MoeLayer]:
+    expert_layers = {d.layer for d in descs
+                     if d.kind in (TaskKind.EXPERT_GATE_UP, TaskKind.EXPERT_DOWN)}
+    out: dict[int, MoeLayer] = {}
+    for d in descs:
+        if d.layer not in expert_layers or d.kind not in MOE_KINDS:
+            continue
+        m = out.setdefault(d.layer, MoeLayer(d.layer))
+        {TaskKind.NORM_ROUTER: m.routers, TaskKind.EXPERT_GATE_UP: m.gate_up,
+         TaskKind.EXPERT_DOWN: m.down}[TaskKind(d.kind)].append(d)
+    return out
+
+
+def plan(descs: list[Descriptor], top_k: int = 6, events: list[Event] | None = None,
+         n_xcds: int = N_XCDS) -> list[Segment | MoeCall]:
+    """Cut a descriptor list into runtime segments and MoE calls, in order.
+
+    A MoE layer is a layer with EXPERT_GATE_UP / EXPERT_DOWN tasks; its
+    NORM_ROUTER tasks go with it (a dense layer's NORM_ROUTER tasks stay in the
+    graph). The call takes the place of the layer's first MoE descriptor."""
+    if events is not None:
+        ids = {e.id for e in events}
+        for d in descs:
+            for ev in (d.wait_event, d.signal_event):
+                if ev >= 0 and ev not in ids:
+                    raise ValueError(f"descriptor {d.index}: event {ev} not in the event table")
+    layers = _moe_layers(descs)
+    for m in layers.values():
+        m.check(top_k, n_xcds)
+    done = {m.done_event: m.layer for m in layers.values()}
+
+    steps: list[Segment | MoeCall] = []
+    produced_before: set[int] = set()     # events signalled by earlier steps
+    cur: list[Descriptor] = []
+    seg_events: set[int] = set()
+    emitted: set[int] = set()
+
+    def close_segment():
+        nonlocal cur, seg_events
+        if cur:
+            steps.append(Segment(cur))
+            produced_before.update(seg_events)
+        cur, seg_events = [], set()
+
+    for d in descs:
+        if d.layer in layers and d.kind in MOE_KINDS:
+            if d.layer not in emitted:
+                close_segment()
+                steps.append(MoeCall(d.layer, layers[d.layer]))
+                emitted.add(d.layer)
+                produced_before.update({t.signal_event for t in
+                                        layers[d.layer].routers + layers[d.layer].gate_up +
+                                        layers[d.layer].down if t.signal_event >= 0})
+            continue
+        nd = d
+        if nd.wait_event >= 0 and nd.wait_event in produced_before:
+            # satisfied by stream order: the producer ran in an earlier step
+            nd = replace(nd, wait_event=-1, wait_scope=0, wait_count=0)
+        if d.wait_event in done and d.flags & Flags.FOLD_PARTIALS:
+            nd = replace(nd, flags=int(Flags(nd.flags) & ~Flags.FOLD_PARTIALS))
+        cur.append(replace(nd, index=len(cur)))
+        if d.signal_event >= 0:
+            seg_events.add(d.signal_event)
+    close_segment()
+    return steps
+
+
+class MoeSteps:
+    """Runs the MoE calls of a plan through fleet_moe_layer_decode.
+
+    `layers` maps a graph layer index to a `DeviceLayer`; one decoder (and its
+    workspace) serves all of them, in order, on one stream."""
+
+    def __init__(self, steps: list[Segment | MoeCall], layers: dict, decoder):
+        self.steps = steps
+        self.layers = layers
+        self.decoder = decoder
+        missing = [s.layer for s in steps if isinstance(s, MoeCall) and s.layer not in layers]
+        if missing:
+            raise KeyError(f"no weights for MoE layers {missing}")
+
+    def run(self, x, segment_runner=None, stream=None) -> None:
+        """x: fp32[hidden] residual stream on the device, updated in place.
+        `segment_runner(segment)` runs the non-MoE descriptors (the owning
+        runtime); without one, only MoE calls may appear in the plan."""
+        for s in self.steps:
+            if isinstance(s, MoeCall):
+                self.decoder.decode_into(self.layers[s.layer], x, x, stream=stream)
+            elif segment_runner is not None:
+                segment_runner(s)
+            else:
+                raise RuntimeError("plan has graph segments but no segment_runner")
+
+
+def moe_layer_descriptors(layer: int, wait_event: int, first_event: int, top_k: int = 6,
+                          n_xcds: int = N_XCDS, workers: int = 37) -> tuple[list[Descriptor], int]:
+    """Descriptors of one MoE layer in the reference's shape (a router task per
+    XCD, then gate_up and down per XCD with slot = xcd for xcd < top_k, else a
+    shared half -1, -2), with fresh event ids from `first_event`. Returns the
+    descriptors and the id of the layer's completion event (its last id). Used
+    to build graphs for tests and for callers that emit their own lists."""
+    out: list[Descriptor] = []
+    ev = first_event
+    routed = []
+    for x in range(n_xcds):
+        out.append(Descriptor(TaskKind.NORM_ROUTER, layer, x, wait_event=wait_event,
+                              signal_event=ev, signal_scope=Scope.XCD_LOCAL,
+                              n_split=workers))
+        routed.append(ev)
+        ev += 1
+    chunk = []
+    for x in range(n_xcds):
+        slot = x if x < top_k else -(x - top_k + 1)
+        out.append(Descriptor(TaskKind.EXPERT_GATE_UP, layer, x, wait_event=routed[x],
+                              expert_slot=slot, local_event=ev, kv_chunk=1,
+                              flags=Flags.CHUNK_SIGNAL))
+        chunk.append(ev)
+        ev += 1
+    done = ev
+    for x in range(n_xcds):
+        slot = x if x < top_k else -(x - top_k + 1)
+        out.append(Descriptor(TaskKind.EXPERT_DOWN, layer, x, wait_event=chunk[x],
+                              signal_event=done, signal_scope=Scope.GLOBAL,
+                              expert_slot=slot, local_event=chunk[x], kv_chunk=1,
+                              flags=Flags.CHUNK_WAIT | Flags.ROUTING_CACHED))
+    return out, done
+
+
+def field_offsets() -> dict[str, int]:
+    """Byte offset of every named field in the packed descriptor."""
+    offs, off = {}, 0
+    for n in FIELD_NAMES:
+        offs[n] = off
+        off += 2 if n != "index" else 4
+    return offs
+
+
+__all__ = ["DESCRIPTOR_BYTES", "FIELD_NAMES", "TaskKind", "Flags", "Scope", "Descriptor",
+           "Event", "MoeLayer", "Segment", "MoeCall", "MoeSteps", "pack_all", "unpack_all",
+           "parse_events", "plan", "moe_layer_descriptors", "field_offsets"]
