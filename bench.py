@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true")
+    ap.add_argument("--no-column", action="store_true",
+                    help="skip config 3 (27-layer FFN column, 29.8 GB of weights)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the known-size kernels that scale rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE: fleet_moe_stream_read over 256 MiB and a 64 MiB fill, "
@@ -215,6 +217,10 @@ def main() -> int:
 
     if not args.no_grouped:
         result["grouped"] = bench_grouped(torch, dev, stream, layer, dims, x_host)
+    if not args.no_column:
+        del layer
+        torch.cuda.empty_cache()
+        result["ffn_column"] = bench_column(torch, dev, stream, dims)
     result["stream_read"] = stream_ceiling(torch, dev, stream, lib)
     if args.calibrate:
         n = 256 << 20
@@ -233,6 +239,63 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(blob, lay, x_host[:K], args.cpu_seconds, gpu_ids)
     print(json.dumps(result), flush=True)
     return 0 if status == 0 else 1
+
+
+def bench_column(torch, dev, stream, dims, n_tok: int = 32, warm: int = 4):
+    """Config 3: the FFN half of all 27 layers (dense layer 0 + 26 MoE layers)
+    chained at batch 1 over 32 seeded tokens, weights drawn on the device.
+    Also times the dense layer alone (its own roofline)."""
+    from fleet_moe import layout as lay_mod, ops, synth, synth_gpu
+    lay = lay_mod.column_layout(dims, n_layers=27)
+    blob = torch.empty(lay.nbytes, dtype=torch.uint8, device=dev)
+    synth_gpu.fill_column(blob, lay, seed=0)
+    col = ops.FfnColumn(blob, lay, dims)
+    xs = synth.hidden_inputs(3, n_tok + warm)
+    xs = ((xs.view(np.uint32) + 0x7FFF + ((xs.view(np.uint32) >> 16) & 1))
+          & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    xd = torch.from_numpy(xs).to(dev)
+    for t in range(warm):
+        col.run_into(xd[t], stream)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for t in range(warm, warm + n_tok):
+        col.run_into(xd[t], stream)
+    b.record(stream)
+    torch.cuda.synchronize()
+    us_tok = a.elapsed_time(b) * 1e3 / n_tok
+    # dense layer 0 alone, back to back
+    y = torch.empty_like(xd[0])
+    nd = 50
+    c = torch.cuda.Event(enable_timing=True)
+    d = torch.cuda.Event(enable_timing=True)
+    c.record(stream)
+    for t in range(nd):
+        col.layer_into(0, xd[t % (n_tok + warm)], y, stream)
+    d.record(stream)
+    torch.cuda.synchronize()
+    us_dense = c.elapsed_time(d) * 1e3 / nd
+    dense_bytes = 3 * lay_mod.DENSE_INTER * dims.hidden * 2
+    moe_bytes = 6 * 3 * dims.hidden * dims.moe_inter * 2 + 3 * dims.hidden * dims.shared_inter * 2
+    tok_bytes = dense_bytes + 26 * (moe_bytes + dims.n_routed * dims.hidden * 2)
+    status = col.status()
+    out = {
+        "workload": "27-layer FFN column (dense layer 0 + 26 MoE layers), batch 1, "
+                    f"{n_tok} chained tokens, weights N(0,0.02^2) bf16 drawn on the device "
+                    "(BASELINE config 3)",
+        "us_per_token": round(us_tok, 1), "tokens_per_s": round(1e6 / us_tok, 1),
+        "bytes_per_token": tok_bytes,
+        "hbm_gbs": round(tok_bytes / (us_tok * 1e-6) / 1e9, 1),
+        "hbm_frac": round(tok_bytes / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "dense_layer": {"us": round(us_dense, 2), "bytes": dense_bytes,
+                        "hbm_gbs": round(dense_bytes / (us_dense * 1e-6) / 1e9, 1),
+                        "hbm_frac": round(dense_bytes / (us_dense * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        "status": status,
+    }
+    del col, blob, xd
+    torch.cuda.empty_cache()
+    return out
 
 
 def stream_ceiling(torch, dev, stream, lib):

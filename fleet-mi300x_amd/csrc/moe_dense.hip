@@ -1,0 +1,236 @@
+// Batch-1 dense SwiGLU layer of DeepSeek-V2-Lite (layer 0, intermediate 10944):
+// x_out = bf16(x + down(bf16(bf16(silu(bf16(g))) * bf16(u)))), g/u = gate/up
+// rows . rms_norm(x), in ONE launch of 256 workgroups (one per CU, 8 waves).
+//
+// What it replaces in the reference: the DENSE_GATE_UP / DENSE_DOWN task
+// bodies of the persistent decode kernel (src/kernels/fleet_kernel.hip:891-903,
+// emitted by src/host/taskgraph.py:444-474) and the layer's NORM_ROUTER
+// prologue; semantics of src/host/reference_decode.py:290-302 (dense_mlp =
+// mlp_unit at the dense width, bf16 residual add).
+//
+//   prologue  RMSNorm exactly as the MoE decode kernel computes it (fp64 sum of
+//             squares, correctly rounded sqrt and division), x_norm as packed
+//             bf16 in registers.
+//   phase G   the 10944 gate/up row pairs (interleaved, 8 KB each) are dealt
+//             round-robin to the 256 workgroups (42 or 43 each); the 8 waves
+//             pull them from an LDS ticket, one in flight per wave, and publish
+//             h as tagged words (epoch << 16 | bf16) with device-scope stores.
+//   phase D   workgroup w owns output rows [8w, 8w + 8): wave r streams row
+//             8w + r (21,888 B) into registers, then the workgroup polls the
+//             10944 h words once into LDS (bf16) and every wave takes its dot.
+// Every wait is bounded and records FLEET_MOE_ABORT_UNIT_WAIT instead of
+// hanging; the last workgroup to exit advances the epoch.
+#include <stddef.h>
+
+#include "moe_common.h"
+
+namespace fleet_moe {
+namespace dense {
+
+constexpr int kDenseInter = 10944;
+constexpr int kWG = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kLanes;
+constexpr int kRowsPerWG = kHidden / kWG;                  // 8 down rows per workgroup
+constexpr int kDnChunks = kDenseInter / kChunk;             // 1368 chunks per down row
+constexpr int kDnIters = (kDnChunks + kLanes - 1) / kLanes; // 22
+constexpr int kPollUnits = kDenseInter / 4;                 // 16-byte units of h words
+static_assert(kRowsPerWG == kWaves, "one down row per wave");
+static_assert(kDenseInter % 4 == 0, "h polled in 16-byte units");
+
+struct Workspace {
+    uint32_t epoch;
+    uint32_t exits;
+    uint32_t abort;
+    uint32_t pad0[61];
+    uint32_t h[kDenseInter];   // (epoch & 0xffff) << 16 | bf16 h
+};
+static_assert(offsetof(Workspace, abort) == 8, "status word offset");
+static_assert(offsetof(Workspace, h) % 16 == 0, "h is read with 16-byte loads");
+
+struct Params {
+    const uint16_t* norm;      // bf16[H] or null
+    const uint16_t* w;         // [2I][H] interleaved gate/up, then [H][I] down
+    const float* x;
+    float* x_out;
+    uint16_t* mlp_out;         // bf16[H] or null
+    Workspace* ws;
+    float eps;
+};
+
+struct Lds {
+    alignas(16) uint32_t xb[kHidden / 2];
+    double red[kWaves];
+    alignas(16) uint32_t hb[kDenseInter / 2];   // h as bf16 pairs
+    int next;
+};
+
+__device__ __forceinline__ int pairs_of(int wg) {
+    return kDenseInter / kWG + (wg < kDenseInter % kWG ? 1 : 0);   // 43 or 42
+}
+
+__device__ __forceinline__ void issue_pair(const u32x4* base, int lane, u32x4 (&b)[8]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        b[m] = ld_stream(base + lane + kLanes * m);
+        b[4 + m] = ld_stream(base + kRowChunks + lane + kLanes * m);
+    }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
+    __shared__ Lds L;
+    const int wg = blockIdx.x, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & (kLanes - 1);
+    Workspace* ws = P.ws;
+    const uint32_t epoch = ld_agent(&ws->epoch) + 1u;
+    const uint32_t tag = (epoch & 0xffffu) << 16;
+    const float4 xv = reinterpret_cast<const float4*>(P.x)[tid];
+    const uint2 gb = P.norm ? reinterpret_cast<const uint2*>(P.norm)[tid]
+                            : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
+    const u32x4* gu = reinterpret_cast<const u32x4*>(P.w);
+    const int n_items = pairs_of(wg);
+    u32x4 buf[8];
+    int cur = wave < n_items ? wave : -1;
+    if (cur >= 0) issue_pair(gu + (int64_t)(wg + kWG * cur) * 2 * kRowChunks, lane, buf);
+    if (tid == 0) L.next = kWaves;
+
+    // RMSNorm (identical arithmetic to the MoE decode kernel)
+    double ss = (double)xv.x * xv.x + (double)xv.y * xv.y + (double)xv.z * xv.z +
+                (double)xv.w * xv.w;
+    ss = wave_sum64(ss);
+    if (lane == 0) L.red[wave] = ss;
+    __syncthreads();
+    double ssq = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) ssq += L.red[w];
+    const float var = (float)(ssq / (double)kHidden);
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(var + P.eps));
+    float y[4] = {bf16r(xv.x * inv), bf16r(xv.y * inv), bf16r(xv.z * inv), bf16r(xv.w * inv)};
+    y[0] = bf16r(y[0] * bf_lo(gb.x));
+    y[1] = bf16r(y[1] * bf_hi(gb.x));
+    y[2] = bf16r(y[2] * bf_lo(gb.y));
+    y[3] = bf16r(y[3] * bf_hi(gb.y));
+    L.xb[2 * tid] = bf16_bits(y[0]) | (bf16_bits(y[1]) << 16);
+    L.xb[2 * tid + 1] = bf16_bits(y[2]) | (bf16_bits(y[3]) << 16);
+    __syncthreads();
+    u32x4 xq[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
+
+    // Phase G
+    auto claim = [&]() -> int {
+        int t = 0;
+        if (lane == 0)
+            t = __hip_atomic_fetch_add(&L.next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        t = wave_bcast(t);
+        return t < n_items ? t : -1;
+    };
+    while (cur >= 0) {
+        const int nxt = claim();
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            g = dot8_d2(buf[m], xq[m], g);
+            u = dot8_d2(buf[4 + m], xq[m], u);
+        }
+        g = wave_sum(g);
+        u = wave_sum(u);
+        if (lane == 0) {
+            const float h = bf16r(bf16r(silu_rn(bf16r(g))) * bf16r(u));
+            st_agent(&ws->h[wg + kWG * cur], tag | bf16_bits(h));
+        }
+        if (nxt >= 0) issue_pair(gu + (int64_t)(wg + kWG * nxt) * 2 * kRowChunks, lane, buf);
+        cur = nxt;
+    }
+
+    // Phase D: this wave's down row in flight before the h wait
+    const int n = kRowsPerWG * wg + wave;
+    const u32x4* drow = gu + (int64_t)2 * kDenseInter * kRowChunks + (int64_t)n * kDnChunks;
+    u32x4 W[kDnIters];
+#pragma unroll
+    for (int i = 0; i < kDnIters; ++i) {
+        const int c = lane + kLanes * i;
+        W[i] = c < kDnChunks ? ld_stream(drow + c) : u32x4{0u, 0u, 0u, 0u};
+    }
+    // h, polled once per workgroup (16 bytes = four words per step)
+    const __amdgpu_buffer_rsrc_t rh = rsrc(ws->h);
+    bool ok = true;
+    for (int k = tid; k < kPollUnits; k += kThreads) {
+        u32x4 v;
+        for (uint32_t it = 0;; ++it) {
+            v = ld_dev16(rh, 16 * k);
+            if ((v.x & 0xffff0000u) == tag && (v.y & 0xffff0000u) == tag &&
+                (v.z & 0xffff0000u) == tag && (v.w & 0xffff0000u) == tag)
+                break;
+            if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&ws->abort) != 0)) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (!ok) break;
+        L.hb[2 * k] = (v.x & 0xffffu) | (v.y << 16);
+        L.hb[2 * k + 1] = (v.z & 0xffffu) | (v.w << 16);
+    }
+    if (!ok)
+        __hip_atomic_fetch_or(&ws->abort, FLEET_MOE_ABORT_UNIT_WAIT, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDnIters; ++i) {
+        const int c = lane + kLanes * i;
+        if (c < kDnChunks) acc = dot8_d2(W[i], reinterpret_cast<const u32x4*>(L.hb)[c], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        const float out = bf16r(acc);
+        P.x_out[n] = bf16r(P.x[n] + out);
+        if (P.mlp_out) P.mlp_out[n] = (uint16_t)bf16_bits(out);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&ws->epoch, epoch);
+    }
+}
+
+}  // namespace dense
+}  // namespace fleet_moe
+
+using namespace fleet_moe;
+
+int fleet_moe_check_dims(const fleet_moe_dims* d);
+int fleet_moe_check_device(int min_cus);
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+extern "C" size_t fleet_moe_dense_workspace_bytes(const fleet_moe_dims* dims, int32_t dense_inter) {
+    if (fleet_moe_check_dims(dims) != 0 || dense_inter != dense::kDenseInter) return 0;
+    return (sizeof(dense::Workspace) + 255) & ~(size_t)255;
+}
+
+extern "C" int fleet_moe_dense_decode(const uint16_t* norm, const uint16_t* w, int32_t dense_inter,
+                                      const float* x, float* x_out, uint16_t* mlp_out,
+                                      void* workspace, size_t workspace_bytes,
+                                      const fleet_moe_dims* dims, hipStream_t stream) {
+    if (int e = fleet_moe_check_dims(dims)) return e;
+    if (dense_inter != dense::kDenseInter) return FLEET_MOE_ERR_DIMS;
+    if (!w || !x || !x_out || !workspace) return FLEET_MOE_ERR_ARG;
+    if (!aligned(w, 16) || !aligned(x, 16) || !aligned(x_out, 16) || !aligned(workspace, 256) ||
+        (norm && !aligned(norm, 8)) || (mlp_out && !aligned(mlp_out, 2)))
+        return FLEET_MOE_ERR_ARG;
+    if (workspace_bytes < sizeof(dense::Workspace)) return FLEET_MOE_ERR_WORKSPACE;
+    if (int e = fleet_moe_check_device(dense::kWG)) return e;
+    dense::Params P;
+    P.norm = norm;
+    P.w = w;
+    P.x = x;
+    P.x_out = x_out;
+    P.mlp_out = mlp_out;
+    P.ws = static_cast<dense::Workspace*>(workspace);
+    P.eps = dims->rms_eps;
+    hipLaunchKernelGGL(dense::dense_kernel, dim3(dense::kWG), dim3(dense::kThreads), 0, stream, P);
+    return (int)hipGetLastError();
+}

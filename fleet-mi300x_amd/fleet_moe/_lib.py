@@ -43,6 +43,10 @@ SYMBOLS = [
     ("fleet_moe_layer_decode", c_int,
      [POINTER(FleetMoeLayer), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
       c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_moe_dense_workspace_bytes", c_size_t, [POINTER(FleetMoeDims), c_int32]),
+    ("fleet_moe_dense_decode", c_int,
+     [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+      POINTER(FleetMoeDims), c_void_p]),
     ("fleet_moe_grouped_workspace_bytes", c_size_t, [POINTER(FleetMoeDims), c_int32]),
     ("fleet_moe_grouped", c_int,
      [POINTER(FleetMoeLayer), c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -135,6 +135,33 @@ def moe_layout(dims: MoeDims = DSV2_LITE, layers=(1,), with_norm: bool = True) -
     return lay
 
 
+DENSE_INTER = 10944     # DeepSeek-V2-Lite intermediate_size (dense layer 0)
+
+
+def column_layout(dims: MoeDims = DSV2_LITE, n_layers: int = 27, first_k_dense: int = 1,
+                  dense_inter: int = DENSE_INTER) -> Layout:
+    """The FFN tensors of a whole decoder stack in pack_weights.py:110-146
+    order: per layer norm_post, then `L{i}.dense` (layers < first_k_dense:
+    interleaved gate/up [2 I][H] then down [H][I]) or router, experts, shared."""
+    lay = Layout()
+    H = dims.hidden
+    for i in range(n_layers):
+        lay.add(f"L{i}.norm_post", (H,))
+        if i < first_k_dense:
+            lay.add(f"L{i}.dense", (3 * dense_inter * H,))
+        else:
+            lay.add(f"L{i}.router", (dims.n_routed, H))
+            lay.add(f"L{i}.experts", (dims.n_routed * dims.expert_stride,))
+            lay.add(f"L{i}.shared", (dims.shared_elems,))
+    lay.scalars.update({
+        "bytes": lay.nbytes, "expert_stride": dims.expert_stride, "hidden": H,
+        "moe_inter": dims.moe_inter, "n_routed": dims.n_routed, "n_shared": dims.n_shared,
+        "top_k": dims.top_k, "rms_eps": dims.rms_eps, "routed_scaling": float(dims.routed_scaling),
+        "layers": n_layers, "first_k_dense": first_k_dense, "dense_inter": dense_inter,
+    })
+    return lay
+
+
 def dims_from_scalars(s: dict) -> MoeDims:
     """MoeDims from manifest scalars."""
     return MoeDims(hidden=int(s["hidden"]), moe_inter=int(s["moe_inter"]),

@@ -196,3 +196,68 @@ def moe(layer: DeviceLayer, x_norm: torch.Tensor, runner: GroupedRunner, stream=
     logits, ids, ws = route(layer, x_norm, stream=stream)
     out = runner.run(layer, f32_to_bf16_bits(x_norm), ids, ws, stream)
     return {"logits": logits, "ids": ids, "weights": ws, "out": out}
+
+
+class DenseDecoder:
+    """Batch-1 dense SwiGLU layer (fleet_moe_dense_decode) with its own
+    workspace: x_out = bf16(x + mlp(rms_norm(x)))."""
+
+    def __init__(self, dims: MoeDims = DSV2_LITE, dense_inter: int = 10944, device="cuda"):
+        self.dims = dims
+        self.dense_inter = int(dense_inter)
+        self._dims = c_dims(dims)
+        n = _lib.load().fleet_moe_dense_workspace_bytes(ctypes.byref(self._dims),
+                                                        self.dense_inter)
+        if n == 0:
+            raise ValueError(f"unsupported dense width {dense_inter}")
+        self.workspace = torch.zeros(n, dtype=torch.uint8, device=device)
+
+    def decode_into(self, norm_ptr: int | None, dense_ptr: int, x: torch.Tensor,
+                    x_out: torch.Tensor, mlp_out: torch.Tensor | None = None, stream=None) -> None:
+        rc = _lib.load().fleet_moe_dense_decode(
+            norm_ptr, dense_ptr, self.dense_inter, _ptr(x), _ptr(x_out), _ptr(mlp_out),
+            _ptr(self.workspace), self.workspace.numel(), ctypes.byref(self._dims),
+            _stream(stream))
+        _lib.check(rc, "fleet_moe_dense_decode")
+
+    def status(self, stream=None) -> int:
+        v = ctypes.c_uint32(0)
+        rc = _lib.load().fleet_moe_workspace_status(_ptr(self.workspace), ctypes.byref(v),
+                                                    _stream(stream))
+        _lib.check(rc, "fleet_moe_workspace_status")
+        return int(v.value)
+
+
+class FfnColumn:
+    """The FFN half of every decoder layer of a stack, chained at batch 1:
+    x <- bf16(x + ffn_L(rms_norm_L(x))) for L = 0 .. layers-1, dense for
+    L < first_k_dense, MoE after (the benchmark's config 3; reference_decode.py:
+    294-302 without the attention half). `blob` is the packed uint8 device
+    tensor of `layout` (fleet_moe.layout.column_layout)."""
+
+    def __init__(self, blob: torch.Tensor, layout: Layout, dims: MoeDims = DSV2_LITE):
+        self.blob, self.layout, self.dims = blob, layout, dims
+        self.n_layers = int(layout.scalars["layers"])
+        self.first_k_dense = int(layout.scalars["first_k_dense"])
+        self.moe = {i: DeviceLayer(blob, layout, i, dims)
+                    for i in range(self.first_k_dense, self.n_layers)}
+        self.decoder = LayerDecoder(dims, device=blob.device)
+        self.dense = DenseDecoder(dims, int(layout.scalars["dense_inter"]), device=blob.device)
+
+    def _addr(self, name: str) -> int:
+        return self.blob.data_ptr() + self.layout.tensors[name].offset
+
+    def layer_into(self, i: int, x: torch.Tensor, x_out: torch.Tensor, stream=None) -> None:
+        if i < self.first_k_dense:
+            self.dense.decode_into(self._addr(f"L{i}.norm_post"), self._addr(f"L{i}.dense"),
+                                   x, x_out, stream=stream)
+        else:
+            self.decoder.decode_into(self.moe[i], x, x_out, stream=stream)
+
+    def run_into(self, x: torch.Tensor, stream=None) -> None:
+        """All layers in place on x (fp32[hidden] on the device); no allocation."""
+        for i in range(self.n_layers):
+            self.layer_into(i, x, x, stream)
+
+    def status(self) -> int:
+        return self.decoder.status() | self.dense.status()

@@ -96,6 +96,25 @@ int fleet_moe_layer_decode(const fleet_moe_layer* layer, const float* x, float* 
                            void* workspace, size_t workspace_bytes,
                            const fleet_moe_dims* dims, hipStream_t stream);
 
+/* Workspace bytes fleet_moe_dense_decode needs (dense_inter = 10944). */
+size_t fleet_moe_dense_workspace_bytes(const fleet_moe_dims* dims, int32_t dense_inter);
+
+/* Batch-1 dense SwiGLU layer (DeepSeek-V2-Lite layer 0, first_k_dense = 1):
+ * x_out = bf16(x + mlp(rms_norm(x))), mlp(v) = down(bf16(bf16(silu(bf16(gate v)))
+ * * bf16(up v))). Replaces the layer's NORM_ROUTER prologue and the
+ * DENSE_GATE_UP (8) / DENSE_DOWN (9) task bodies (src/kernels/fleet_kernel.hip:
+ * 891-903; src/host/taskgraph.py:444-474); semantics of src/host/
+ * reference_decode.py:290-302 (dense_mlp, residual add).
+ * norm: post-attention RMSNorm weight bf16[hidden] or NULL (unit); w: the
+ * packed "L0.dense" block, [2*dense_inter][hidden] gate/up interleaved then
+ * [hidden][dense_inter] down (src/host/pack_weights.py:143-146); x, x_out:
+ * fp32[hidden] (may be equal); mlp_out: bf16[hidden] or NULL. One launch over
+ * every CU. */
+int fleet_moe_dense_decode(const uint16_t* norm, const uint16_t* w, int32_t dense_inter,
+                           const float* x, float* x_out, uint16_t* mlp_out, void* workspace,
+                           size_t workspace_bytes, const fleet_moe_dims* dims,
+                           hipStream_t stream);
+
 /* Workspace bytes fleet_moe_grouped needs for up to max_tokens tokens. */
 size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, int32_t max_tokens);
 

@@ -333,6 +333,19 @@ def moe_layer(layer: PackedLayer, x, top_k: int = TOP_K,
     return r
 
 
+def dense_layer(gate, up, down, x, gamma=None, eps: float = RMS_EPS) -> dict:
+    """A dense decoder layer's FFN half: x' = bf16(x + mlp(rms_norm(x))).
+
+    reference_decode.py:290-291 (dense_mlp = mlp_unit at the dense width) and
+    :301-302 (post-attention norm, bf16 residual add); gate/up [I][H], down
+    [H][I] as fp32 arrays of bf16 values. Returns dict(x_n, out, x_out).
+    """
+    x = np.asarray(x, np.float32)
+    x_n = rms_norm(x, gamma, eps)
+    out = mlp_unit(gate, up, down, x_n)
+    return {"x_n": x_n, "out": out, "x_out": bf16_round(x + out)}
+
+
 # ---------------------------------------------------------------- a8 grouped
 
 def moe_grouped(layer: PackedLayer, x_n, ids, weights, combine_rule: str = "decode") -> dict:

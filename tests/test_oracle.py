@@ -229,6 +229,29 @@ def test_mlp_unit_special_cases():
                                [0.0, 1 / (1 + np.exp(-1)), -2 / (1 + np.exp(2))], rtol=1e-7)
 
 
+def test_dense_layer_matches_torch_hf_decoder_ffn_half():
+    """Dense layer 0: torch runs DeepseekV2RMSNorm, DeepseekV2MLP at the dense
+    width and the bf16 residual add of DeepseekV2DecoderLayer; the oracle's
+    dense_layer must agree to bf16 tolerance, element-exact on most."""
+    rng = np.random.default_rng(12)
+    H, I = 2048, 10944
+    gate = R(0.02 * rng.standard_normal((I, H)).astype(np.float32))
+    up = R(0.02 * rng.standard_normal((I, H)).astype(np.float32))
+    down = R(0.02 * rng.standard_normal((H, I)).astype(np.float32))
+    gamma = R(1.0 + 0.1 * rng.standard_normal(H).astype(np.float32))
+    x = R(rng.standard_normal((2, H)).astype(np.float32))
+    got = orc.dense_layer(gate, up, down, x, gamma)
+    xn = hf_rmsnorm_bf16(x, gamma, 1e-6)
+    out = hf_mlp_bf16(gate, up, down, xn)
+    want = (t_bf16(x) + t_bf16(out)).to(torch.float32).numpy()
+    assert rel_err(got["out"], out) <= 1e-2
+    assert rel_err(got["x_out"], want) <= 1e-2
+    assert np.mean(got["x_out"] == want) > 0.95
+    # zero weights leave the residual stream unchanged
+    z = orc.dense_layer(np.zeros_like(gate), up, down, x[0], gamma)
+    np.testing.assert_array_equal(z["x_out"], x[0])
+
+
 # ---------------------------------------------------------------- a4 packed layout
 
 def pack_tiny(rng, H, I, E, n_shared, std):
