@@ -412,17 +412,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) er[m] = P.router[(int64_t)wg * kRowChunks + lane + kLanes * m];
     }
-    // The control wave has no pair in flight: it streams this workgroup's
-    // eight shared-expert down rows (44 KB, routing-independent) straight
-    // into LDS while the routing is being settled.
-    if (ctl) {
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(
-                                 P.shared + (int64_t)2 * kSharedInter * kHidden) +
-                             (int64_t)wg * kSharedBlockBytes + lane * 16;
-#pragma unroll 4
-        for (int k = 0; k < kSharedBlockBytes / 1024; ++k)
-            __builtin_amdgcn_global_load_lds(src + k * 1024, L.sdown + k * 1024, 16, 0, 0);
-    }
     u32x4 bufA[8];
     int cur;
     if (!ctl)
@@ -548,6 +537,18 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         __builtin_amdgcn_s_setprio(0);
         FLEET_TRACE(10);
         if (exact_row && !exact_sel) publish_exact_row(P, er, xq, wg, epoch);
+        // This workgroup's eight shared-expert down rows (44 KB, needed in
+        // phase D) go straight into LDS now. Issued any earlier they would
+        // push the wave past the 63 loads a wave can have outstanding and
+        // stall the RMSNorm / routing path on the first load's return.
+        {
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(
+                                     P.shared + (int64_t)2 * kSharedInter * kHidden) +
+                                 (int64_t)wg * kSharedBlockBytes + lane * 16;
+#pragma unroll 4
+            for (int k = 0; k < kSharedBlockBytes / 1024; ++k)
+                __builtin_amdgcn_global_load_lds(src + k * 1024, L.sdown + k * 1024, 16, 0, 0);
+        }
         cur = claim();
         if (cur >= 0) issue(cur, bufA);
     }
