@@ -33,6 +33,7 @@ that does not retype its formula.
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -419,3 +420,146 @@ def moe_bytes(hidden: int = HIDDEN, moe_inter: int = MOE_INTER, top_k: int = TOP
     n = top_k if distinct is None else int(distinct)
     return {"expert": per_expert, "shared": shared, "router": router,
             "selected": n * per_expert + shared}
+
+
+# ---------------------------------------------------------------- full decode (config 4)
+# The attention half of a decoder layer, the embedding and the lm_head, so the
+# 27-layer decode can be checked end to end. Shapes of DeepSeek-V2-Lite
+# (reference/dsv2lite_config.json); RoPE is YaRN as that config states it
+# (theta 1e4, factor 40, original context 4096, beta 32 / 1, mscale 0.707 on
+# both sides).
+
+HEADS = 16
+KV_LORA = 512
+QK_NOPE = 128
+QK_ROPE = 64
+V_HEAD = 128
+VOCAB = 102400
+ROPE_THETA = 1e4
+ROPE_FACTOR = 40.0
+ROPE_ORIG_MAX = 4096
+BETA_FAST, BETA_SLOW = 32.0, 1.0
+MSCALE = MSCALE_ALL_DIM = 0.707
+
+
+def yarn_mscale(scale: float, m: float) -> float:
+    """reference_decode.py:78-82 (HF yarn_get_mscale)."""
+    return 1.0 if scale <= 1 else 0.1 * m * math.log(scale) + 1.0
+
+
+def rope_tables(max_pos: int, dim: int = QK_ROPE, base: float = ROPE_THETA,
+                scale: float = ROPE_FACTOR, original_max: int = ROPE_ORIG_MAX,
+                beta_fast: float = BETA_FAST, beta_slow: float = BETA_SLOW,
+                mscale: float = MSCALE, mscale_all_dim: float = MSCALE_ALL_DIM):
+    """cos, sin [max_pos][dim] fp32: DeepseekV2YarnRotaryEmbedding's cache
+    (reference_decode.py:85-117): inverse frequencies blended between the
+    extrapolated and the interpolated ones by a linear ramp over the
+    correction range, angles t * inv_freq duplicated over both halves, times
+    mscale(scale, mscale) / mscale(scale, mscale_all_dim)."""
+    def corr_dim(rot):
+        return (dim * math.log(original_max / (rot * 2 * math.pi))) / (2 * math.log(base))
+    lo = max(math.floor(corr_dim(beta_fast)), 0)
+    hi = min(math.ceil(corr_dim(beta_slow)), dim - 1)
+    if lo == hi:
+        hi += 0.001
+    half = np.arange(0, dim, 2, dtype=np.float32)
+    extra = 1.0 / (base ** (half / dim))
+    inter = 1.0 / (scale * base ** (half / dim))
+    ramp = np.clip((np.arange(dim // 2, dtype=np.float32) - lo) / (hi - lo), 0, 1)
+    keep = 1.0 - ramp                     # weight of the extrapolated frequency
+    inv_freq = inter * (1 - keep) + extra * keep
+    t = np.arange(max_pos, dtype=np.float32)
+    ang = np.outer(t, inv_freq)
+    emb = np.concatenate([ang, ang], axis=-1)
+    m = yarn_mscale(scale, mscale) / yarn_mscale(scale, mscale_all_dim)
+    return (np.cos(emb) * m).astype(np.float32), (np.sin(emb) * m).astype(np.float32)
+
+
+def apply_rope(x, cos, sin) -> np.ndarray:
+    """DeepseekV2 RoPE (reference_decode.py:120-134): reorder [x0, x1, ..., x63]
+    to [x0, x2, ..., x62, x1, x3, ..., x63], then x * cos + rotate_half(x) * sin
+    with rotate_half(v) = [-v[32:], v[:32]]. The result stays in the reordered
+    basis (that is what HF caches and what the queries meet)."""
+    x = np.asarray(x, np.float32)
+    d = x.shape[-1]
+    y = np.concatenate([x[..., 0::2], x[..., 1::2]], axis=-1)
+    rot = np.concatenate([-y[..., d // 2:], y[..., :d // 2]], axis=-1)
+    return (y * cos + rot * sin).astype(np.float32)
+
+
+def softmax_scale() -> float:
+    """reference_decode.py:191-197: (qk_nope + qk_rope)^-0.5 * mscale_all_dim^2."""
+    m = yarn_mscale(ROPE_FACTOR, MSCALE_ALL_DIM)
+    return (QK_NOPE + QK_ROPE) ** -0.5 * m * m
+
+
+@dataclass
+class AttnLayer:
+    """One layer's attention tensors in the packed layout (bf16 bits):
+    norm_in [H], qkv [(heads*(nope+rope)) + kv_lora + rope][H] (q_proj rows
+    then kv_a_proj_with_mqa rows), kv_a_norm [kv_lora], kv_b
+    [heads*(nope+v)][kv_lora], o_proj [H][heads*v] (pack_weights.py:113-121)."""
+    norm_in: np.ndarray
+    qkv: np.ndarray
+    kv_a_norm: np.ndarray
+    kv_b: np.ndarray
+    o_proj: np.ndarray
+    heads: int = HEADS
+    cache_f32: dict = field(default_factory=dict, repr=False)
+
+    def f32(self, name):
+        if name not in self.cache_f32:
+            self.cache_f32[name] = bf16_to_f32(getattr(self, name))
+        return self.cache_f32[name]
+
+
+def attention(w: AttnLayer, x, cache, pos: int, cos, sin, eps: float = RMS_EPS) -> dict:
+    """Absorbed-MLA decode step (reference_decode.py:210-256), bf16 rounding
+    points as there: q and kv_a bf16, c after kv_a_layernorm and k_pe after
+    RoPE bf16 (written to cache[pos]), q_c / scores / softmax / o_c in fp32,
+    the 2048 head outputs bf16, o_proj bf16. cache: fp32 [max_pos][576],
+    rows < pos filled. Returns dict(out, q_c, scores, row)."""
+    H = w.heads
+    L, Dk, Dr, Dv = KV_LORA, QK_NOPE, QK_ROPE, V_HEAD
+    hidden = np.asarray(x).shape[-1]
+    x_n = rms_norm(x, bf16_to_f32(w.norm_in), eps)
+    qkv = bf16_round(w.f32("qkv").reshape(-1, hidden) @ x_n)
+    q = qkv[: H * (Dk + Dr)].reshape(H, Dk + Dr)
+    kv_a = qkv[H * (Dk + Dr):]
+    c_new = rms_norm(kv_a[:L], bf16_to_f32(w.kv_a_norm), eps)
+    k_pe = bf16_round(apply_rope(kv_a[L:], cos[pos], sin[pos]))
+    q_pe = bf16_round(apply_rope(q[:, Dk:], cos[pos], sin[pos]))
+    cache[pos, :L] = c_new
+    cache[pos, L:] = k_pe
+    C = cache[: pos + 1, :L]
+    KP = cache[: pos + 1, L:]
+    kv_b = w.f32("kv_b").reshape(H * (Dk + Dv), L)
+    scale = np.float32(softmax_scale())
+    out = np.empty(H * Dv, np.float32)
+    qcs, scs = [], []
+    for h in range(H):
+        w_uk = kv_b[h * (Dk + Dv): h * (Dk + Dv) + Dk]
+        w_uv = kv_b[h * (Dk + Dv) + Dk: (h + 1) * (Dk + Dv)]
+        q_c = q[h, :Dk] @ w_uk
+        s = (C @ q_c + KP @ q_pe[h]) * scale
+        p = np.exp(s - s.max())
+        p = p / p.sum()
+        out[h * Dv:(h + 1) * Dv] = w_uv @ (p @ C)
+        qcs.append(q_c)
+        scs.append(s)
+    o = bf16_round(w.f32("o_proj").reshape(hidden, H * Dv) @ bf16_round(out))
+    return {"out": o, "q_c": np.array(qcs), "scores": np.array(scs),
+            "row": cache[pos].copy()}
+
+
+def lm_head_argmax(x, final_norm, lm_head, eps: float = RMS_EPS) -> dict:
+    """Final RMSNorm, logits = bf16(lm_head . x_n) (fleet_kernel.hip:915-920,
+    EPI_BF16), next token = the largest logit, lowest index on ties (the
+    argmax rule of fleet_kernel.hip:509-585)."""
+    x_n = rms_norm(x, None if final_norm is None else bf16_to_f32(final_norm), eps)
+    W = lm_head if lm_head.dtype == np.float32 else bf16_to_f32(lm_head)
+    logits = bf16_round(W.reshape(-1, x_n.shape[-1]) @ x_n)
+    best = float(logits.max())
+    tok = int(np.flatnonzero(logits == best)[0])
+    second = float(np.max(np.where(np.arange(logits.size) == tok, -np.inf, logits)))
+    return {"logits": logits, "token": tok, "margin": best - second}
