@@ -221,4 +221,4 @@ extern "C" const char* fleet_moe_error_string(int code) {
     }
 }
 
-extern "C" int fleet_moe_abi_version(void) { return 100; }
+extern "C" int fleet_moe_abi_version(void) { return 101; }

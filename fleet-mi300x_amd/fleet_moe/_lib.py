@@ -19,6 +19,8 @@ ERR_DEVICE = 10004
 ABORT_ROUTER_WAIT = 0x1
 ABORT_UNIT_WAIT = 0x2
 ABORT_GROUP_WAIT = 0x4
+ABORT_POSITION = 0x8
+ABORT_TOKEN = 0x10
 
 
 class FleetMoeDims(ctypes.Structure):
@@ -32,6 +34,12 @@ class FleetMoeLayer(ctypes.Structure):
     """struct fleet_moe_layer (device pointers)."""
     _fields_ = [("norm", c_void_p), ("router", c_void_p), ("experts", c_void_p),
                 ("expert_stride", c_int64), ("shared", c_void_p)]
+
+
+class FleetAttnLayer(ctypes.Structure):
+    """struct fleet_attn_layer (device pointers)."""
+    _fields_ = [("norm_in", c_void_p), ("qkv", c_void_p), ("kv_a_norm", c_void_p),
+                ("kv_b", c_void_p), ("o_proj", c_void_p)]
 
 
 # (name, restype, argtypes) of every symbol the header declares.
@@ -50,6 +58,14 @@ SYMBOLS = [
     ("fleet_moe_grouped_workspace_bytes", c_size_t, [POINTER(FleetMoeDims), c_int32]),
     ("fleet_moe_grouped", c_int,
      [POINTER(FleetMoeLayer), c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+      c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_attn_workspace_bytes", c_size_t, [POINTER(FleetMoeDims)]),
+    ("fleet_attn_decode", c_int,
+     [POINTER(FleetAttnLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+      c_void_p, c_void_p, c_void_p, c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_embed", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    ("fleet_lm_head_argmax", c_int,
+     [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
       c_size_t, POINTER(FleetMoeDims), c_void_p]),
     ("fleet_moe_stream_read", c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
     ("fleet_moe_workspace_status", c_int, [c_void_p, POINTER(c_uint32), c_void_p]),

@@ -162,6 +162,55 @@ def column_layout(dims: MoeDims = DSV2_LITE, n_layers: int = 27, first_k_dense: 
     return lay
 
 
+VOCAB = 102400          # DeepSeek-V2-Lite vocab_size
+ATTN_HEADS = 16
+KV_LORA = 512
+QK_NOPE = 128
+QK_ROPE = 64
+V_HEAD = 128
+QKV_ROWS = ATTN_HEADS * (QK_NOPE + QK_ROPE) + KV_LORA + QK_ROPE    # 3648
+
+# YaRN scalars of the manifest (pack_weights.py:171-181), DeepSeek-V2-Lite values
+ROPE_SCALARS = {"rope_theta": 10000.0, "rope_factor": 40.0, "rope_original_max": 4096,
+                "beta_fast": 32.0, "beta_slow": 1.0, "mscale": 0.707, "mscale_all_dim": 0.707}
+
+
+def model_layout(dims: MoeDims = DSV2_LITE, n_layers: int = 27, first_k_dense: int = 1,
+                 dense_inter: int = DENSE_INTER, vocab: int = VOCAB) -> Layout:
+    """Every tensor of the decoder in pack_weights.py:106-146 order: embed,
+    final_norm, lm_head, then per layer norm_in, norm_post, qkv (q_proj rows
+    then kv_a_proj_with_mqa rows, [3648][H]), kv_a_norm [512], kv_b
+    [16 * (128 + 128)][512], o_proj [H][16 * 128], then the FFN tensors as in
+    column_layout."""
+    lay = Layout()
+    H = dims.hidden
+    lay.add("embed", (vocab, H))
+    lay.add("final_norm", (H,))
+    lay.add("lm_head", (vocab, H))
+    for i in range(n_layers):
+        lay.add(f"L{i}.norm_in", (H,))
+        lay.add(f"L{i}.norm_post", (H,))
+        lay.add(f"L{i}.qkv", (QKV_ROWS, H))
+        lay.add(f"L{i}.kv_a_norm", (KV_LORA,))
+        lay.add(f"L{i}.kv_b", (ATTN_HEADS * (QK_NOPE + V_HEAD), KV_LORA))
+        lay.add(f"L{i}.o_proj", (H, ATTN_HEADS * V_HEAD))
+        if i < first_k_dense:
+            lay.add(f"L{i}.dense", (3 * dense_inter * H,))
+        else:
+            lay.add(f"L{i}.router", (dims.n_routed, H))
+            lay.add(f"L{i}.experts", (dims.n_routed * dims.expert_stride,))
+            lay.add(f"L{i}.shared", (dims.shared_elems,))
+    lay.scalars.update({
+        "bytes": lay.nbytes, "expert_stride": dims.expert_stride, "hidden": H,
+        "layers": n_layers, "first_k_dense": first_k_dense, "moe_inter": dims.moe_inter,
+        "dense_inter": dense_inter, "n_routed": dims.n_routed, "n_shared": dims.n_shared,
+        "top_k": dims.top_k, "heads": ATTN_HEADS, "kv_lora": KV_LORA, "qk_nope": QK_NOPE,
+        "qk_rope": QK_ROPE, "v_head": V_HEAD, "vocab": vocab, "rms_eps": dims.rms_eps,
+        "routed_scaling": float(dims.routed_scaling), **ROPE_SCALARS,
+    })
+    return lay
+
+
 def dims_from_scalars(s: dict) -> MoeDims:
     """MoeDims from manifest scalars."""
     return MoeDims(hidden=int(s["hidden"]), moe_inter=int(s["moe_inter"]),

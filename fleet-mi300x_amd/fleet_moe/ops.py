@@ -261,3 +261,152 @@ class FfnColumn:
 
     def status(self) -> int:
         return self.decoder.status() | self.dense.status()
+
+
+class AttnDecoder:
+    """Absorbed-MLA attention half of a layer, the embedding and lm_head +
+    argmax (fleet_attn_decode / fleet_embed / fleet_lm_head_argmax), sharing
+    one persistent workspace. Calls must be ordered on one stream."""
+
+    def __init__(self, dims: MoeDims = DSV2_LITE, device="cuda"):
+        self.dims = dims
+        self._dims = c_dims(dims)
+        n = _lib.load().fleet_attn_workspace_bytes(ctypes.byref(self._dims))
+        self.workspace = torch.zeros(n, dtype=torch.uint8, device=device)
+
+    def attn_into(self, layer: "_lib.FleetAttnLayer", x: torch.Tensor, x_out: torch.Tensor,
+                  cache: torch.Tensor, pos: int = 0, pos_dev: torch.Tensor | None = None,
+                  cos: torch.Tensor = None, sin: torch.Tensor = None, stream=None) -> None:
+        """x_out = bf16(x + attention(x)) at position `pos` (or *pos_dev);
+        cache: int16 [max_pos][576] of this layer."""
+        rc = _lib.load().fleet_attn_decode(
+            ctypes.byref(layer), _ptr(x), _ptr(x_out), _ptr(cache), int(cache.shape[0]),
+            int(pos), _ptr(pos_dev), _ptr(cos), _ptr(sin), _ptr(self.workspace),
+            self.workspace.numel(), ctypes.byref(self._dims), _stream(stream))
+        _lib.check(rc, "fleet_attn_decode")
+
+    def embed_into(self, embed_ptr: int, token: torch.Tensor, x: torch.Tensor, stream=None):
+        rc = _lib.load().fleet_embed(embed_ptr, _ptr(token), _ptr(x), _ptr(self.workspace),
+                                     self.workspace.numel(), _stream(stream))
+        _lib.check(rc, "fleet_embed")
+
+    def lm_head_into(self, x: torch.Tensor, final_norm_ptr: int | None, lm_head_ptr: int,
+                     logits: torch.Tensor | None = None, token_out: torch.Tensor | None = None,
+                     token_next: torch.Tensor | None = None,
+                     pos_advance: torch.Tensor | None = None, stream=None) -> None:
+        rc = _lib.load().fleet_lm_head_argmax(
+            _ptr(x), final_norm_ptr, lm_head_ptr, _ptr(logits), _ptr(token_out),
+            _ptr(token_next), _ptr(pos_advance), _ptr(self.workspace), self.workspace.numel(),
+            ctypes.byref(self._dims), _stream(stream))
+        _lib.check(rc, "fleet_lm_head_argmax")
+
+    def status(self, stream=None) -> int:
+        v = ctypes.c_uint32(0)
+        rc = _lib.load().fleet_moe_workspace_status(_ptr(self.workspace), ctypes.byref(v),
+                                                    _stream(stream))
+        _lib.check(rc, "fleet_moe_workspace_status")
+        return int(v.value)
+
+
+class Decoder:
+    """Batch-1 greedy decode of the whole model on the GPU.
+
+    `blob` is the packed uint8 device tensor of `layout`
+    (fleet_moe.layout.model_layout). Per token (reference_decode.py:294-302
+    per layer, the launcher's step order fleet_kernel.hip:966-1040):
+    x = embed[token]; for each layer x = bf16(x + attn(x)), then
+    x = bf16(x + ffn(rms_norm(x))) (dense below first_k_dense, MoE above);
+    token = argmax(bf16(lm_head . rms_norm(x))). The KV cache is
+    [layers][max_pos][576] bf16. The token and the position live in device
+    memory (`token`, `pos`), so one step can be captured in a HIP graph and
+    replayed: the argmax writes the next token and advances the position."""
+
+    def __init__(self, blob: torch.Tensor, layout: Layout, dims: MoeDims = DSV2_LITE,
+                 max_pos: int = 4096):
+        from .rope import RopeParams, yarn_tables
+        self.blob, self.layout, self.dims = blob, layout, dims
+        dev = blob.device
+        self.n_layers = int(layout.scalars["layers"])
+        self.max_pos = int(max_pos)
+        cos, sin = yarn_tables(self.max_pos, RopeParams.from_scalars(layout.scalars))
+        self.cos = torch.from_numpy(cos).to(dev)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.cache = torch.zeros((self.n_layers, self.max_pos, 576), dtype=torch.int16,
+                                 device=dev)
+        self.ffn = FfnColumn(blob, layout, dims)
+        self.attn = AttnDecoder(dims, device=dev)
+        self.attn_layers = [self._attn_layer(i) for i in range(self.n_layers)]
+        self.x = torch.zeros(dims.hidden, dtype=torch.float32, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)      # input of the next step
+        self.token_out = torch.zeros(1, dtype=torch.int32, device=dev)  # last pick
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)        # position of the next step
+        self.graph = None
+
+    def _addr(self, name: str) -> int:
+        return self.blob.data_ptr() + self.layout.tensors[name].offset
+
+    def _attn_layer(self, i: int) -> _lib.FleetAttnLayer:
+        return _lib.FleetAttnLayer(self._addr(f"L{i}.norm_in"), self._addr(f"L{i}.qkv"),
+                                   self._addr(f"L{i}.kv_a_norm"), self._addr(f"L{i}.kv_b"),
+                                   self._addr(f"L{i}.o_proj"))
+
+    def layer_into(self, i: int, x: torch.Tensor, pos: int = 0, use_pos_dev: bool = False,
+                   stream=None) -> None:
+        """Layer i in place on x (attention half, then FFN half)."""
+        self.attn.attn_into(self.attn_layers[i], x, x, self.cache[i], pos,
+                            self.pos if use_pos_dev else None, self.cos, self.sin, stream)
+        self.ffn.layer_into(i, x, x, stream)
+
+    def enqueue_step(self, logits: torch.Tensor | None = None, feed_back: bool = True,
+                     stream=None) -> None:
+        """One token from device state: embed(*token), every layer at *pos,
+        lm_head + argmax -> token_out (and -> token when feed_back), *pos += 1.
+        No allocation, no synchronisation: capturable."""
+        self.attn.embed_into(self._addr("embed"), self.token, self.x, stream)
+        for i in range(self.n_layers):
+            self.layer_into(i, self.x, use_pos_dev=True, stream=stream)
+        self.attn.lm_head_into(self.x, self._addr("final_norm"), self._addr("lm_head"), logits,
+                               self.token_out, self.token if feed_back else None, self.pos,
+                               stream)
+
+    def reset(self, pos: int = 0) -> None:
+        self.pos.fill_(int(pos))
+
+    def capture(self) -> None:
+        """Capture enqueue_step() into a HIP graph (replayed by step())."""
+        s = torch.cuda.Stream(device=self.blob.device)
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.enqueue_step(stream=s)
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = g
+
+    def step(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.enqueue_step()
+
+    def prefill(self, tokens: torch.Tensor) -> None:
+        """Teacher-forced steps over tokens (device int32 [n]) from position 0:
+        fills the cache rows 0..n-1; after it token_out holds the pick after
+        the last prompt token and pos == n."""
+        self.reset(0)
+        for i in range(tokens.numel()):
+            self.token.copy_(tokens[i:i + 1])
+            self.step()
+
+    def generate(self, n: int) -> torch.Tensor:
+        """n greedy tokens continuing from the state prefill() left: the first
+        input is token_out. Returns the device int32 [n] of picks."""
+        out = torch.empty(n, dtype=torch.int32, device=self.blob.device)
+        self.token.copy_(self.token_out)
+        for j in range(n):
+            self.step()
+            out[j:j + 1].copy_(self.token_out)
+        return out
+
+    def status(self) -> int:
+        return self.attn.status() | self.ffn.status()

@@ -15,7 +15,7 @@ from .layout import DSV2_LITE, Layout, MoeDims
 
 STD = 0.02
 ROUTER, EXPERT_GATE, EXPERT_UP, EXPERT_DOWN, SHARED_GATE, SHARED_UP, SHARED_DOWN, \
-    DENSE_GATE, DENSE_UP, DENSE_DOWN = range(10)
+    DENSE_GATE, DENSE_UP, DENSE_DOWN, EMBED, LM_HEAD, QKV, KV_B, O_PROJ = range(15)
 
 
 def _key(seed: int, layer: int, kind: int, index: int) -> int:
@@ -68,3 +68,32 @@ def fill_column(blob: torch.Tensor, lay: Layout, seed: int = 0, dims: MoeDims = 
                       e, dev)
         _fill_mlp(view("shared"), dims.shared_inter, H, seed, i,
                   (SHARED_GATE, SHARED_UP, SHARED_DOWN), 0, dev)
+
+
+def fill_model(blob: torch.Tensor, lay: Layout, seed: int = 0, dims: MoeDims = DSV2_LITE) -> None:
+    """Write every tensor of a whole-model layout (fleet_moe.layout.model_layout):
+    the FFN tensors as fill_column does, then embed, lm_head and each layer's
+    qkv, kv_b and o_proj drawn N(0, 0.02^2); final_norm, norm_in and kv_a_norm
+    are 1.0 (HF's initial RMSNorm weight)."""
+    fill_column(blob, lay, seed, dims)
+    dev = blob.device
+    words = blob.view(torch.int16)
+    one = torch.tensor(1.0, dtype=torch.bfloat16).view(torch.int16).item()
+
+    def view(name):
+        t = lay.tensors[name]
+        return words[t.offset // 2: (t.offset + t.nbytes) // 2]
+
+    def draw(name, layer, kind):
+        v = view(name)
+        v[:] = _normal_bf16((v.numel(),), seed, layer, kind, 0, dev)
+
+    draw("embed", -1, EMBED)
+    draw("lm_head", -1, LM_HEAD)
+    view("final_norm").fill_(one)
+    for i in range(int(lay.scalars["layers"])):
+        view(f"L{i}.norm_in").fill_(one)
+        view(f"L{i}.kv_a_norm").fill_(one)
+        draw(f"L{i}.qkv", i, QKV)
+        draw(f"L{i}.kv_b", i, KV_B)
+        draw(f"L{i}.o_proj", i, O_PROJ)

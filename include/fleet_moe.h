@@ -136,6 +136,75 @@ int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens, const int3
                       void* workspace, size_t workspace_bytes, const fleet_moe_dims* dims,
                       hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * The rest of a decoder layer and of the decode step (absorbed MLA attention,
+ * embedding, lm_head + argmax), so that the full 27-layer batch-1 decode runs
+ * on this library: per token, embed, then per layer fleet_attn_decode and
+ * fleet_moe_dense_decode / fleet_moe_layer_decode, then fleet_lm_head_argmax.
+ * Fixed shape: 16 heads, kv_lora 512, qk_nope 128, qk_rope 64, v_head 128,
+ * vocab 102400, max_pos <= 4096. */
+
+/* One layer's attention weights: the per-layer pointer tables of Weights
+ * (src/runtime/fleet_types.h:44-59: layer_norm_in, layer_qkv,
+ * layer_kv_a_norm, layer_kv_b, layer_o_proj), i.e. the manifest tensors
+ * "L{i}.norm_in", "L{i}.qkv" ([q_proj (3072) ; kv_a_proj_with_mqa (576)]
+ * rows of hidden), "L{i}.kv_a_norm", "L{i}.kv_b" ([16 * 256][512]),
+ * "L{i}.o_proj" ([hidden][2048]) (src/host/pack_weights.py:113-121). */
+typedef struct fleet_attn_layer {
+    const uint16_t* norm_in;    /* bf16[hidden] or NULL (unit) */
+    const uint16_t* qkv;        /* bf16[3648][hidden] */
+    const uint16_t* kv_a_norm;  /* bf16[512] or NULL (unit) */
+    const uint16_t* kv_b;       /* bf16[4096][512] */
+    const uint16_t* o_proj;     /* bf16[hidden][2048] */
+} fleet_attn_layer;
+
+/* Workspace bytes fleet_attn_decode, fleet_embed and fleet_lm_head_argmax
+ * need (one workspace serves all three; about 2.2 MB). */
+size_t fleet_attn_workspace_bytes(const fleet_moe_dims* dims);
+
+/* The attention half of one decoder layer at one position:
+ * x_out = bf16(x + o_proj(mla(rms_norm(x, norm_in)))). Replaces the
+ * QKV_FUSED (kind 0), Q_ABSORB (14), ATTENTION (1), MERGE_UV (2) and O_PROJ
+ * (3) task bodies (src/kernels/fleet_kernel.hip:647-660, 675-704, 706-803,
+ * 805-830; src/kernels/attention.h:62-93, 171-222, 230-350, 358-420);
+ * semantics of src/host/reference_decode.py:210-256 (attention_absorbed) and
+ * :294-298 (the residual add). Writes this layer's cache row at the position
+ * (c after kv_a_layernorm, then k_pe after RoPE, 576 bf16) and attends over
+ * rows 0..position of `cache` ([max_pos][576] bf16: KVCache.data of one
+ * layer, src/runtime/fleet_types.h:107-111). rope_cos / rope_sin:
+ * fp32[max_pos][64] YaRN tables (the reference's act.cos / act.sin,
+ * src/host/fleet_launch.hip:186-218). x, x_out: fp32[hidden] (may be equal).
+ * The position is `pos` (0 <= pos < max_pos <= 4096, checked here) or, when
+ * pos_dev is not NULL, the device int32 *pos_dev read by the kernels, so one
+ * captured graph serves every step; a device position outside [0, max_pos)
+ * sets FLEET_MOE_ABORT_POSITION in the workspace status and leaves x_out
+ * unspecified. Five launches on `stream`. */
+int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, float* x_out,
+                      uint16_t* cache, int32_t max_pos, int32_t pos, const int32_t* pos_dev,
+                      const float* rope_cos, const float* rope_sin, void* workspace,
+                      size_t workspace_bytes, const fleet_moe_dims* dims, hipStream_t stream);
+
+/* x = embed[*token] as fp32 (the EMBED task, src/kernels/fleet_kernel.hip:
+ * 68-78). token: a device int32, so a decode loop can feed the previous
+ * step's argmax without a host round trip; a token outside [0, 102400) sets
+ * FLEET_MOE_ABORT_TOKEN in the (attention) workspace status and x = 0. */
+int fleet_embed(const uint16_t* embed, const int32_t* token, float* x, void* workspace,
+                size_t workspace_bytes, hipStream_t stream);
+
+/* Greedy next token: logits = bf16(lm_head . rms_norm(x, final_norm)), token
+ * = argmax with ties to the lowest index. Replaces the LM_HEAD (11) and
+ * ARGMAX (12) task bodies (src/kernels/fleet_kernel.hip:905-920, 509-585);
+ * semantics of HF's bf16 lm_head and torch.argmax as src/host/
+ * reference_run.py:99-105 picks the greedy token. logits: fp32[102400]
+ * (bf16-valued) or NULL; token_out, token_next: device int32 or NULL (both
+ * receive the token; token_next is the input of the next fleet_embed, NULL
+ * under teacher forcing); pos_advance: device int32 incremented by one after
+ * the pick (the pos_dev of the next step) or NULL. Two launches. */
+int fleet_lm_head_argmax(const float* x, const uint16_t* final_norm, const uint16_t* lm_head,
+                         float* logits, int32_t* token_out, int32_t* token_next,
+                         int32_t* pos_advance, void* workspace, size_t workspace_bytes,
+                         const fleet_moe_dims* dims, hipStream_t stream);
+
 /* Copies the workspace's sticky status word to *status (0 = healthy; a
  * nonzero value names a bounded wait that expired, see FLEET_MOE_ABORT_*),
  * synchronising `stream`. The reference's equivalent is the sticky rt.abort
@@ -145,6 +214,8 @@ int fleet_moe_workspace_status(const void* workspace, uint32_t* status, hipStrea
 #define FLEET_MOE_ABORT_ROUTER_WAIT 0x1u  /* router logits never published  */
 #define FLEET_MOE_ABORT_UNIT_WAIT 0x2u    /* an expert unit never completed */
 #define FLEET_MOE_ABORT_GROUP_WAIT 0x4u   /* grouped step phase never completed */
+#define FLEET_MOE_ABORT_POSITION 0x8u     /* device position outside [0, max_pos) */
+#define FLEET_MOE_ABORT_TOKEN 0x10u       /* device token outside the vocabulary */
 
 /* Diagnostic: reads `bytes` of device memory with the weight-streaming load
  * pattern of the kernels above (16-byte non-temporal loads, 1 KB per wave

@@ -563,3 +563,61 @@ def lm_head_argmax(x, final_norm, lm_head, eps: float = RMS_EPS) -> dict:
     tok = int(np.flatnonzero(logits == best)[0])
     second = float(np.max(np.where(np.arange(logits.size) == tok, -np.inf, logits)))
     return {"logits": logits, "token": tok, "margin": best - second}
+
+
+@dataclass
+class DenseFfn:
+    """A dense layer's FFN (pack_weights.py:143-146, unpacked): gate, up
+    [I][H] and down [H][I] as fp32 arrays of bf16 values; norm is the
+    post-attention RMSNorm weight (bf16 bits) or None."""
+    gate: np.ndarray
+    up: np.ndarray
+    down: np.ndarray
+    norm: np.ndarray | None = None
+
+
+def decoder_layer(attn_w: AttnLayer, ffn, x, cache, pos: int, cos, sin,
+                  eps: float = RMS_EPS) -> dict:
+    """One decoder layer, reference_decode.py:294-302: x1 = bf16(x + attn(x)),
+    then x2 = bf16(x1 + ffn(rms_norm(x1, norm_post))) with the MoE of
+    `moe_layer` (ffn a PackedLayer) or the dense MLP (ffn a DenseFfn).
+    Appends cache[pos]. Returns dict(x_attn, x_out, ids)."""
+    a = attention(attn_w, x, cache, pos, cos, sin, eps)
+    x1 = bf16_round(np.asarray(x, np.float32) + a["out"])
+    if isinstance(ffn, DenseFfn):
+        g = None if ffn.norm is None else bf16_to_f32(ffn.norm)
+        r = dense_layer(ffn.gate, ffn.up, ffn.down, x1, g, eps)
+        ids = None
+    else:
+        r = moe_layer(ffn, x1, eps=eps)
+        ids = r["ids"]
+    return {"x_attn": x1, "x_out": r["x_out"], "ids": ids}
+
+
+@dataclass
+class DecodeModel:
+    """The whole decoder for `decode_step`: embed / lm_head bf16 bits
+    [vocab][H] (lm_head may be pre-widened fp32), final_norm bf16 bits or
+    None, and per layer an AttnLayer and a PackedLayer or DenseFfn."""
+    embed: np.ndarray
+    final_norm: np.ndarray | None
+    lm_head: np.ndarray
+    attn: list
+    ffn: list
+
+
+def decode_step(model: DecodeModel, token: int, pos: int, caches, cos, sin,
+                eps: float = RMS_EPS) -> dict:
+    """One greedy step at position `pos`: x = embed[token] (fp32 of the bf16
+    row, fleet_kernel.hip:68-78), every decoder_layer, then lm_head_argmax.
+    caches: per layer fp32 [max_pos][576], row pos appended. Returns
+    dict(token, margin, logits, x per layer output)."""
+    hidden = model.attn[0].norm_in.size
+    x = bf16_to_f32(model.embed.reshape(-1, hidden)[int(token)])
+    xs = []
+    for i, (aw, fw) in enumerate(zip(model.attn, model.ffn)):
+        x = decoder_layer(aw, fw, x, caches[i], pos, cos, sin, eps)["x_out"]
+        xs.append(x)
+    r = lm_head_argmax(x, model.final_norm, model.lm_head, eps)
+    r["xs"] = xs
+    return r

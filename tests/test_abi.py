@@ -17,7 +17,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "fleet_moe.h"
 
 def declared_functions() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"\b(fleet_moe_\w+)\s*\(", text))
+    return set(re.findall(r"\b(fleet_\w+)\s*\(", text))
 
 
 @pytest.fixture(scope="module")
@@ -39,10 +39,12 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_lib.FleetMoeDims) == 28
     assert ctypes.sizeof(_lib.FleetMoeLayer) == 40
     assert _lib.FleetMoeLayer.expert_stride.offset == 24
+    # fleet_attn_layer: 5 pointers
+    assert ctypes.sizeof(_lib.FleetAttnLayer) == 40
 
 
 def test_version_and_error_strings(lib):
-    assert lib.fleet_moe_abi_version() == 100
+    assert lib.fleet_moe_abi_version() == 101
     assert b"shape" in lib.fleet_moe_error_string(_lib.ERR_DIMS)
     assert b"workspace" in lib.fleet_moe_error_string(_lib.ERR_WORKSPACE)
     assert lib.fleet_moe_error_string(0) == b"success"
@@ -101,3 +103,34 @@ def test_bad_pointers_rejected_without_device(lib):
     assert lib.fleet_moe_grouped(ctypes.byref(layer), 8, 256, 256, 256, 256, 256, small,
                                  ctypes.byref(d), None) == _lib.ERR_WORKSPACE
     assert lib.fleet_moe_workspace_status(None, None, None) == _lib.ERR_ARG
+
+
+def test_attention_entry_points_reject_bad_arguments_without_device(lib):
+    d = c_dims(DSV2_LITE)
+    n = lib.fleet_attn_workspace_bytes(ctypes.byref(d))
+    assert n % 256 == 0 and (1 << 20) < n < (4 << 20)
+    assert lib.fleet_attn_workspace_bytes(ctypes.byref(c_dims(MoeDims(hidden=4096)))) == 0
+    layer = _lib.FleetAttnLayer(256, 256, 256, 256, 256)
+    args = dict(x=256, x_out=256, cache=256, max_pos=128, pos=0, pos_dev=None, cos=256, sin=256,
+                ws=256, ws_bytes=n)
+
+    def call(layer_=layer, dims=d, **kw):
+        a = {**args, **kw}
+        return lib.fleet_attn_decode(ctypes.byref(layer_), a["x"], a["x_out"], a["cache"],
+                                     a["max_pos"], a["pos"], a["pos_dev"], a["cos"], a["sin"],
+                                     a["ws"], a["ws_bytes"], ctypes.byref(dims), None)
+
+    assert call(x=None) == _lib.ERR_ARG
+    assert call(pos=128) == _lib.ERR_ARG                 # host position past max_pos
+    assert call(pos=-1) == _lib.ERR_ARG
+    assert call(max_pos=4097) == _lib.ERR_ARG            # beyond the cache the kernels index
+    assert call(cache=258) == _lib.ERR_ARG               # misaligned
+    assert call(layer_=_lib.FleetAttnLayer(256, None, 256, 256, 256)) == _lib.ERR_ARG
+    assert call(ws_bytes=n - 256) == _lib.ERR_WORKSPACE
+    assert call(dims=c_dims(MoeDims(moe_inter=1024))) == _lib.ERR_DIMS
+    assert lib.fleet_embed(None, 256, 256, 256, n, None) == _lib.ERR_ARG
+    assert lib.fleet_embed(256, 256, 256, 256, 64, None) == _lib.ERR_WORKSPACE
+    assert lib.fleet_lm_head_argmax(256, None, None, None, None, None, None, 256, n,
+                                    ctypes.byref(d), None) == _lib.ERR_ARG
+    assert lib.fleet_lm_head_argmax(256, None, 256, None, 258, None, None, 256, n,
+                                    ctypes.byref(d), None) == _lib.ERR_ARG

@@ -1,0 +1,238 @@
+"""GPU parity of the attention half of a decoder layer (fleet_attn_decode),
+the embedding (fleet_embed) and lm_head + argmax (fleet_lm_head_argmax)
+against the CPU oracle, at the DeepSeek-V2-Lite shape (16 heads, kv_lora 512,
+qk_nope 128, qk_rope 64, v_head 128, hidden 2048, vocab 102400).
+
+Each attention call is teacher-forced: the oracle gets the same input x and
+the same cache rows. Inside a call the checks are split by kind:
+* the q / kv_a GEMV (fp32 accumulation in another order) within bf16
+  tolerance;
+* everything downstream of it recomputed by the oracle from the GPU's own
+  q / kv_a, bit for bit: the appended cache row (kv_a_layernorm, RoPE of k_pe)
+  and the rotated q_pe; the absorbed query q_c at fp32 tolerance;
+* the layer output x_out = bf16(x + o_proj(...)) within bf16 tolerance
+  (rel 1e-2, >= 95% of elements bit-equal).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from fleet_moe import _lib, ops, rope  # noqa: E402
+from fleet_moe.layout import DSV2_LITE  # noqa: E402
+from oracle import moe_oracle as orc  # noqa: E402
+
+H, NH, L, DK, DR, DV, V = 2048, 16, 512, 128, 64, 128, 102400
+QKV_ROWS = NH * (DK + DR) + L + DR
+MAX_POS = 1100
+WS_QKV = 256                                   # byte offsets of workspace arrays
+WS_QC = WS_QKV + 4 * QKV_ROWS
+WS_QPE = WS_QC + 4 * NH * L
+
+
+def say(msg: str) -> None:
+    print(f"[gpu] {msg}", flush=True)
+
+
+def rel_err(got, want) -> float:
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def bits(a) -> np.ndarray:
+    return orc.bf16_bits(np.asarray(a, np.float32))
+
+
+def dev16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+
+
+def ws_f32(dec: ops.AttnDecoder, off: int, n: int) -> np.ndarray:
+    return dec.workspace[off: off + 4 * n].view(torch.float32).cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def attn_setup():
+    rng = np.random.default_rng(11)
+    w = orc.AttnLayer(
+        norm_in=bits(1 + 0.1 * rng.standard_normal(H, dtype=np.float32)),
+        qkv=bits(0.02 * rng.standard_normal((QKV_ROWS, H), dtype=np.float32)),
+        kv_a_norm=bits(1 + 0.1 * rng.standard_normal(L, dtype=np.float32)),
+        kv_b=bits(0.02 * rng.standard_normal((NH * (DK + DV), L), dtype=np.float32)),
+        o_proj=bits(0.02 * rng.standard_normal((H, NH * DV), dtype=np.float32)))
+    d = {k: dev16(getattr(w, k)) for k in ("norm_in", "qkv", "kv_a_norm", "kv_b", "o_proj")}
+    layer = _lib.FleetAttnLayer(*(d[k].data_ptr() for k in
+                                  ("norm_in", "qkv", "kv_a_norm", "kv_b", "o_proj")))
+    cos, sin = rope.yarn_tables(MAX_POS)
+    # cache rows as a decode would leave them: normalised c, rotated k_pe
+    cache = orc.bf16_round(rng.standard_normal((MAX_POS, L + DR), dtype=np.float32))
+    return {"w": w, "dev": d, "layer": layer, "cos": cos, "sin": sin,
+            "cos_d": torch.from_numpy(cos).cuda(), "sin_d": torch.from_numpy(sin).cuda(),
+            "cache": cache, "rng": rng}
+
+
+def _x(rng) -> np.ndarray:
+    # a residual stream after a few layers: bf16 values of rms ~ 0.5
+    return orc.bf16_round(0.5 * rng.standard_normal(H, dtype=np.float32))
+
+
+def test_attention_layer_matches_oracle(attn_setup):
+    S = attn_setup
+    w, rng, cos, sin = S["w"], S["rng"], S["cos"], S["sin"]
+    host_cache = S["cache"].copy()
+    cache_d = dev16(bits(host_cache))
+    dec = ops.AttnDecoder(DSV2_LITE)
+    qkv_w = orc.bf16_to_f32(w.qkv)
+    for pos in (0, 1, 63, 64, 65, 200, 1023, MAX_POS - 1):
+        say(f"attention pos {pos}")
+        x = _x(rng)
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty_like(xd)
+        dec.attn_into(S["layer"], xd, yd, cache_d, pos, None, S["cos_d"], S["sin_d"])
+        torch.cuda.synchronize()
+        assert dec.status() == 0
+        g_qkv = ws_f32(dec, WS_QKV, QKV_ROWS)
+        g_qc = ws_f32(dec, WS_QC, NH * L).reshape(NH, L)
+        g_qpe = ws_f32(dec, WS_QPE, NH * DR).reshape(NH, DR)
+        g_row = orc.bf16_to_f32(cache_d[pos].cpu().numpy().view(np.uint16))
+        # q / kv_a GEMV
+        x_n = orc.rms_norm(x, orc.bf16_to_f32(w.norm_in))
+        want_qkv = orc.bf16_round(qkv_w @ x_n)
+        assert rel_err(g_qkv, want_qkv) <= 1e-2 and np.mean(g_qkv == want_qkv) > 0.95
+        # downstream of the GPU's own q / kv_a: bit for bit
+        kv_a = g_qkv[NH * (DK + DR):]
+        np.testing.assert_array_equal(
+            g_row[:L], orc.rms_norm(kv_a[:L], orc.bf16_to_f32(w.kv_a_norm)), err_msg="c row")
+        np.testing.assert_array_equal(
+            g_row[L:], orc.bf16_round(orc.apply_rope(kv_a[L:], cos[pos], sin[pos])),
+            err_msg="k_pe row")
+        q = g_qkv[: NH * (DK + DR)].reshape(NH, DK + DR)
+        np.testing.assert_array_equal(
+            g_qpe, orc.bf16_round(orc.apply_rope(q[:, DK:], cos[pos], sin[pos])), err_msg="q_pe")
+        kv_b = orc.bf16_to_f32(w.kv_b).reshape(NH, DK + DV, L)
+        want_qc = np.einsum("hd,hdl->hl", q[:, :DK].astype(np.float64),
+                            kv_b[:, :DK].astype(np.float64))
+        assert rel_err(g_qc, want_qc) <= 1e-5
+        # the layer output, oracle teacher-forced on the same cache rows
+        r = orc.attention(w, x, host_cache, pos, cos, sin)
+        host_cache[pos] = g_row                      # keep both caches identical
+        want = orc.bf16_round(x + r["out"])
+        got = yd.cpu().numpy()
+        assert rel_err(got, want) <= 1e-2, f"pos {pos}"
+        assert np.mean(got == want) > 0.95, f"pos {pos}: {np.mean(got == want)}"
+
+
+def test_attention_in_place_and_device_position_and_graph(attn_setup):
+    """x_out may alias x; a device position gives the same bits as the host
+    position; a captured graph replays at the positions the device holds."""
+    S = attn_setup
+    rng = S["rng"]
+    cache0 = dev16(bits(S["cache"]))
+    dec = ops.AttnDecoder(DSV2_LITE)
+    x = torch.from_numpy(_x(rng)).cuda()
+    positions = (5, 64, 700)
+    want = []
+    for p in positions:
+        c = cache0.clone()
+        y = torch.empty_like(x)
+        dec.attn_into(S["layer"], x, y, c, p, None, S["cos_d"], S["sin_d"])
+        want.append((y.clone(), c[p].clone()))
+    torch.cuda.synchronize()
+    say("device position, in place")
+    pos_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for p, (wy, wrow) in zip(positions, want):
+        c = cache0.clone()
+        y = x.clone()
+        pos_d.fill_(p)
+        dec.attn_into(S["layer"], y, y, c, 0, pos_d, S["cos_d"], S["sin_d"])
+        torch.cuda.synchronize()
+        assert torch.equal(y, wy) and torch.equal(c[p], wrow), f"pos {p}"
+    say("graph replay")
+    c = cache0.clone()
+    y = torch.empty_like(x)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            dec.attn_into(S["layer"], x, y, c, 0, pos_d, S["cos_d"], S["sin_d"], stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(2):
+        for p, (wy, wrow) in zip(positions, want):
+            c.copy_(cache0)
+            pos_d.fill_(p)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, wy) and torch.equal(c[p], wrow), f"replay {rep} pos {p}"
+    assert dec.status() == 0
+
+
+def test_attention_position_checks(attn_setup):
+    S = attn_setup
+    dec = ops.AttnDecoder(DSV2_LITE)
+    x = torch.zeros(H, dtype=torch.float32, device="cuda")
+    c = torch.zeros((64, L + DR), dtype=torch.int16, device="cuda")
+    with pytest.raises(_lib.FleetMoeError):
+        dec.attn_into(S["layer"], x, x, c, 64, None, S["cos_d"], S["sin_d"])
+    pos_d = torch.tensor([64], dtype=torch.int32, device="cuda")
+    dec.attn_into(S["layer"], x, x, c, 0, pos_d, S["cos_d"], S["sin_d"])
+    assert dec.status() & _lib.ABORT_POSITION
+    assert int(torch.count_nonzero(c)) == 0             # nothing written
+
+
+def test_embed_and_token_check():
+    rng = np.random.default_rng(5)
+    E = bits(0.02 * rng.standard_normal((V, H), dtype=np.float32))
+    Ed = dev16(E)
+    dec = ops.AttnDecoder(DSV2_LITE)
+    x = torch.empty(H, dtype=torch.float32, device="cuda")
+    for t in (0, 1, 4097, V - 1):
+        dec.embed_into(Ed.data_ptr(), torch.tensor([t], dtype=torch.int32, device="cuda"), x)
+        np.testing.assert_array_equal(x.cpu().numpy(), orc.bf16_to_f32(E[t]))
+    assert dec.status() == 0
+    dec.embed_into(Ed.data_ptr(), torch.tensor([V], dtype=torch.int32, device="cuda"), x)
+    assert dec.status() & _lib.ABORT_TOKEN
+    assert int(torch.count_nonzero(x)) == 0
+
+
+def test_lm_head_argmax_matches_oracle():
+    rng = np.random.default_rng(6)
+    W = bits(0.02 * rng.standard_normal((V, H), dtype=np.float32))
+    fn = bits(1 + 0.1 * rng.standard_normal(H, dtype=np.float32))
+    Wd, fnd = dev16(W), dev16(fn)
+    Wf = orc.bf16_to_f32(W)
+    dec = ops.AttnDecoder(DSV2_LITE)
+    logits = torch.empty(V, dtype=torch.float32, device="cuda")
+    tok = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    nxt = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    pos = torch.tensor([7], dtype=torch.int32, device="cuda")
+    for trial in range(3):
+        x = orc.bf16_round(rng.standard_normal(H, dtype=np.float32))
+        say(f"lm_head trial {trial}")
+        dec.lm_head_into(torch.from_numpy(x).cuda(), fnd.data_ptr(), Wd.data_ptr(), logits,
+                         tok, nxt, pos)
+        torch.cuda.synchronize()
+        r = orc.lm_head_argmax(x, fn, Wf)
+        g = logits.cpu().numpy()
+        assert np.max(np.abs(g - r["logits"])) <= 2.0 ** -6 * np.max(np.abs(r["logits"]))
+        assert np.mean(g == r["logits"]) > 0.99
+        t = int(tok.item())
+        assert t == int(nxt.item()) == int(np.flatnonzero(g == g.max())[0])
+        if r["margin"] > np.max(np.abs(g - r["logits"])):
+            assert t == r["token"]
+    assert int(pos.item()) == 10
+    # a planted tie: a copy of the best row at a lower index wins
+    best = int(tok.item())
+    lower = best // 2
+    W2 = Wd.clone()
+    W2[lower] = Wd[best]
+    dec.lm_head_into(torch.from_numpy(x).cuda(), fnd.data_ptr(), W2.data_ptr(), None, tok)
+    torch.cuda.synchronize()
+    assert int(tok.item()) == lower
+    assert dec.status() == 0

@@ -119,3 +119,53 @@ def test_lm_head_argmax_lowest_index_and_bf16_logits():
     W2 = np.vstack([W, W[[r["token"]]]])                    # duplicate the best row at the end
     r2 = orc.lm_head_argmax(x, None, W2)
     assert r2["token"] == r["token"] and r2["margin"] == 0.0
+
+
+def _zero_like(w: orc.AttnLayer) -> orc.AttnLayer:
+    return orc.AttnLayer(norm_in=w.norm_in, qkv=w.qkv, kv_a_norm=w.kv_a_norm, kv_b=w.kv_b,
+                         o_proj=np.zeros_like(w.o_proj), heads=w.heads)
+
+
+def test_decoder_layer_composition_special_cases():
+    """o_proj = 0 makes the attention half the identity, so the layer is the
+    FFN half alone; a zero FFN makes the layer the attention half alone."""
+    rng = np.random.default_rng(3)
+    heads, hidden, inter = 2, 256, 64
+    w = _random_attn(rng, heads, hidden)
+    cos, sin = orc.rope_tables(8)
+    x = orc.bf16_round(rng.standard_normal(hidden).astype(np.float32))
+    g = orc.bf16_round(0.05 * rng.standard_normal((inter, hidden)).astype(np.float32))
+    u = orc.bf16_round(0.05 * rng.standard_normal((inter, hidden)).astype(np.float32))
+    d = orc.bf16_round(0.05 * rng.standard_normal((hidden, inter)).astype(np.float32))
+    ffn = orc.DenseFfn(g, u, d)
+    cache = np.zeros((8, orc.KV_LORA + orc.QK_ROPE), np.float32)
+    r = orc.decoder_layer(_zero_like(w), ffn, x, cache, 0, cos, sin)
+    np.testing.assert_array_equal(r["x_attn"], x)
+    np.testing.assert_array_equal(r["x_out"], orc.dense_layer(g, u, d, x)["x_out"])
+    zero = orc.DenseFfn(np.zeros_like(g), np.zeros_like(u), np.zeros_like(d))
+    cache2 = np.zeros_like(cache)
+    r2 = orc.decoder_layer(w, zero, x, cache2, 0, cos, sin)
+    a = orc.attention(w, x, np.zeros_like(cache), 0, cos, sin)["out"]
+    np.testing.assert_array_equal(r2["x_out"], orc.bf16_round(x + a))
+    np.testing.assert_array_equal(r2["x_attn"], r2["x_out"])
+
+
+def test_decode_step_reads_the_token_row_and_picks_it_back():
+    """With one-hot embedding rows, lm_head = embed and a layer that adds
+    nothing, the step maps every token to itself: the embedding is indexed by
+    row and the logits are lm_head rows."""
+    rng = np.random.default_rng(4)
+    heads, hidden, vocab, inter = 2, 256, 40, 32
+    w = _zero_like(_random_attn(rng, heads, hidden))
+    zero = orc.DenseFfn(np.zeros((inter, hidden), np.float32),
+                        np.zeros((inter, hidden), np.float32),
+                        np.zeros((hidden, inter), np.float32))
+    E = np.zeros((vocab, hidden), np.float32)
+    E[np.arange(vocab), rng.permutation(hidden)[:vocab]] = 1.0
+    model = orc.DecodeModel(embed=orc.bf16_bits(E), final_norm=None, lm_head=orc.bf16_bits(E),
+                            attn=[w], ffn=[zero])
+    cos, sin = orc.rope_tables(4)
+    for tok in (0, 7, vocab - 1):
+        caches = [np.zeros((4, orc.KV_LORA + orc.QK_ROPE), np.float32)]
+        r = orc.decode_step(model, tok, 0, caches, cos, sin)
+        assert r["token"] == tok and r["margin"] == pytest.approx(hidden ** 0.5, rel=1e-2)
