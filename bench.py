@@ -49,6 +49,8 @@ def parse_args():
     ap.add_argument("--no-grouped", action="store_true")
     ap.add_argument("--no-column", action="store_true",
                     help="skip config 3 (27-layer FFN column, 29.8 GB of weights)")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip config 4 (27-layer full decode, 31.4 GB of weights)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the known-size kernels that scale rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE: fleet_moe_stream_read over 256 MiB and a 64 MiB fill, "
@@ -221,6 +223,8 @@ def main() -> int:
         del layer
         torch.cuda.empty_cache()
         result["ffn_column"] = bench_column(torch, dev, stream, dims)
+    if not args.no_decode:
+        result["full_decode"] = bench_decode(torch, dev, stream, dims)
     result["stream_read"] = stream_ceiling(torch, dev, stream, lib)
     if args.calibrate:
         n = 256 << 20
@@ -294,6 +298,81 @@ def bench_column(torch, dev, stream, dims, n_tok: int = 32, warm: int = 4):
         "status": status,
     }
     del col, blob, xd
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_decode(torch, dev, stream, dims, prompt_len: int = 1024, n_gen: int = 32):
+    """Config 4: the full 27-layer model (absorbed-MLA attention, dense layer
+    0, 26 MoE layers, lm_head + greedy argmax) at batch 1, weights drawn on the
+    device. The KV cache is prefilled by teacher-forced steps over a seeded
+    uniform prompt of 1024 tokens, then 32 greedy tokens are generated; each
+    step is one replay of the captured HIP graph of the step (the token and
+    the position live on the device, the argmax feeds both forward)."""
+    from fleet_moe import layout as lay_mod, ops, synth_gpu
+    lay = lay_mod.model_layout(dims, n_layers=27)
+    blob = torch.empty(lay.nbytes, dtype=torch.uint8, device=dev)
+    synth_gpu.fill_model(blob, lay, seed=0)
+    max_pos = prompt_len + n_gen
+    dec = ops.Decoder(blob, lay, dims, max_pos=max_pos)
+    prompt = np.random.default_rng(0).integers(0, lay_mod.VOCAB, prompt_len).astype(np.int32)
+    prompt_d = torch.from_numpy(prompt).to(dev)
+    torch.cuda.synchronize()
+    dec.capture()
+    t0 = time.perf_counter()
+    dec.prefill(prompt_d)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    toks = torch.empty(n_gen, dtype=torch.int32, device=dev)
+    dec.token.copy_(dec.token_out)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for j in range(n_gen):
+        dec.graph.replay()
+        toks[j:j + 1].copy_(dec.token_out)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms_tok = a.elapsed_time(b) / n_gen
+    # the same steps launched eagerly (no graph), from the same state
+    dec.graph = None
+    dec.token.copy_(prompt_d[-1:])
+    dec.pos.fill_(prompt_len - 1)
+    dec.step()            # the last prompt step again: same cache row, same first pick
+    c = torch.cuda.Event(enable_timing=True)
+    d = torch.cuda.Event(enable_timing=True)
+    toks_e = torch.empty_like(toks)
+    c.record(stream)
+    for j in range(n_gen):
+        dec.step()
+        toks_e[j:j + 1].copy_(dec.token_out)
+    d.record(stream)
+    torch.cuda.synchronize()
+    ms_tok_eager = c.elapsed_time(d) / n_gen
+    H = dims.hidden
+    attn_bytes = (lay_mod.QKV_ROWS * H + lay_mod.ATTN_HEADS * (lay_mod.QK_NOPE + lay_mod.V_HEAD)
+                  * lay_mod.KV_LORA + H * lay_mod.ATTN_HEADS * lay_mod.V_HEAD) * 2
+    moe_bytes = (6 * 3 * H * dims.moe_inter + 3 * H * dims.shared_inter + dims.n_routed * H) * 2
+    dense_bytes = 3 * lay_mod.DENSE_INTER * H * 2
+    head_bytes = lay_mod.VOCAB * H * 2
+    mean_rows = prompt_len + (n_gen + 1) / 2
+    cache_bytes = int(27 * mean_rows * 576 * 2)
+    tok_bytes = 27 * attn_bytes + 26 * moe_bytes + dense_bytes + head_bytes + cache_bytes
+    out = {
+        "workload": "27-layer DeepSeek-V2-Lite-shape decode, batch 1, absorbed MLA, "
+                    f"KV cache prefilled with {prompt_len} seeded uniform tokens, {n_gen} greedy "
+                    "tokens, weights N(0,0.02^2) bf16 drawn on the device (BASELINE config 4)",
+        "ms_per_token": round(ms_tok, 4), "tokens_per_s": round(1e3 / ms_tok, 1),
+        "ms_per_token_eager": round(ms_tok_eager, 4),
+        "bytes_per_token": tok_bytes,
+        "hbm_gbs": round(tok_bytes / (ms_tok * 1e-3) / 1e9, 1),
+        "hbm_frac": round(tok_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "prefill_s": round(prefill_s, 3),
+        "graph_equals_eager": bool(torch.equal(toks, toks_e)),
+        "tokens_head": [int(t) for t in toks[:8].cpu()],
+        "status": dec.status(),
+    }
+    del dec, blob
     torch.cuda.empty_cache()
     return out
 
