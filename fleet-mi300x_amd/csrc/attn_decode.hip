@@ -6,8 +6,12 @@
 // of the kernel's EMBED / LM_HEAD / ARGMAX tasks (src/kernels/fleet_kernel.hip:
 // 68-78, 509-585, 905-920): bf16 rounding after q / kv_a, after
 // kv_a_layernorm, after RoPE (both the cached k_pe and q_pe), after the
-// concatenated head outputs and after o_proj; q_c, scores, softmax and o_c in
-// fp32; bf16 logits; argmax with the lowest index on ties.
+// concatenated head outputs and after o_proj; bf16 logits; argmax with the
+// lowest index on ties. Every dot product is the exact value rounded once to
+// fp32 (fp64 accumulation of exact products); q_c is that fp32 value; the
+// scores, the softmax and its weighted sum of c stay in fp64 (chunk partials
+// merged in fp64) and o_c is rounded once to fp32, so no result depends on
+// how positions are split into chunks.
 //
 // One layer is five launches on the caller's stream (each reads what the
 // previous one wrote; the kernel boundary orders them):
@@ -16,8 +20,8 @@
 //            W_UK, 1 KB row loads, summed through LDS) and RoPE(q_pe); the 17th
 //            normalises c, rotates k_pe and writes the cache row at pos
 //   mla      16 heads x 64-position chunks: the chunk's 64 scores (a wave per
-//            8 positions, rows held in registers), then its softmax partial
-//            (max, sum of exp, sum exp * c) from the same registers
+//            8 positions, rows held in registers), then its fp64 softmax
+//            partial (max, sum of exp, sum exp * c) from the same registers
 //   combine  16 heads x 8: merge the chunks into o_c, then 16 of the head's 128
 //            outputs of W_UV o_c, bf16
 //   oproj    256 workgroups: 8 rows of o_proj each, bf16, residual add
@@ -67,9 +71,9 @@ struct Workspace {
     float qkv[kQkvRows];                       // bf16-valued
     float qc[kHeads][kLora];                   // absorbed queries
     float qpe[kHeads][kRope];                  // rotated, bf16-valued
-    float part_m[kHeads][kMaxChunks];
-    float part_l[kHeads][kMaxChunks];
-    float part_o[kHeads][kMaxChunks][kLora];
+    double part_m[kHeads][kMaxChunks];         // chunk partials of the softmax, fp64
+    double part_l[kHeads][kMaxChunks];
+    double part_o[kHeads][kMaxChunks][kLora];
     uint16_t out[kHeads * kV];                 // bf16 head outputs
     float cand_v[kWG];                         // lm_head: best logit per workgroup
     int32_t cand_i[kWG];
@@ -127,11 +131,12 @@ __device__ __forceinline__ void load_row(const uint16_t* W, int64_t row, u32x4 (
     for (int m = 0; m < 4; ++m) w[m] = ld_stream(r + lane + kLanes * m);
 }
 
+// Exactly rounded dot of a K = 2048 bf16 row with a bf16 vector (wave total).
 __device__ __forceinline__ float dot_row(const u32x4 (&w)[4], const u32x4 (&xq)[4]) {
-    float a = 0.f;
+    double a = 0.0;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) a = dot8_d2(w[m], xq[m], a);
-    return wave_sum(a);
+    for (int m = 0; m < 4; ++m) a = dot8_x(w[m], xq[m], a);
+    return (float)wave_sum64(a);
 }
 
 // Rows first, first + stride, ... (< end) of a K = 2048 matrix against the
@@ -174,11 +179,18 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_kernel(const float* x, const 
 // v62, v1, v3, .., v63]; out[i] = y[i] cos[i] - y[i+32] sin[i] (i < 32),
 // y[i] cos[i] + y[i-32] sin[i] (i >= 32), two products and a sum, unfused, as
 // the fp32 reference computes them; rounded to bf16. Returns out[i].
+// Contraction is off for these three operations (HIP compiles with
+// -ffp-contract=fast, and its __fmul_rn / __fadd_rn carry that flag into the
+// inlined code): a fused multiply-add rounds twice instead of three times and
+// moves about one result in 2^16 to the neighbouring bf16 value.
 __device__ __forceinline__ float rope_one(const float* v, const float* cs, const float* sn, int i) {
+#pragma clang fp contract(off)
     const int half = kRope / 2;
     const float y = i < half ? v[2 * i] : v[2 * (i - half) + 1];
     const float r = i < half ? -v[2 * i + 1] : v[2 * (i - half)];
-    return bf16r(__fadd_rn(__fmul_rn(y, cs[i]), __fmul_rn(r, sn[i])));
+    const float a = y * cs[i];
+    const float b = r * sn[i];
+    return bf16r(a + b);
 }
 
 // ---------------------------------------------------------------- prep
@@ -191,7 +203,7 @@ __global__ __launch_bounds__(kThreads, 1) void prep_kernel(const uint16_t* kv_b,
                                                            uint16_t* cache, float eps,
                                                            Workspace* ws) {
     __shared__ float v[kLora + kRope];
-    __shared__ alignas(16) float part[kWaves][kLora];
+    __shared__ double part[kWaves][kLora];
     __shared__ double red[kWaves];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
     const int pos = read_pos(P);
@@ -210,25 +222,27 @@ __global__ __launch_bounds__(kThreads, 1) void prep_kernel(const uint16_t* kv_b,
             w[r] = ld_stream(wuk + (int64_t)(kUkRows * wave + r) * (kLora / kChunk) + lane);
         if (tid < kNope + kRope) v[tid] = ws->qkv[h * (kNope + kRope) + tid];
         __syncthreads();
-        // lane holds columns 8 lane .. 8 lane + 7 of this wave's 16 rows
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        // lane holds columns 8 lane .. 8 lane + 7 of this wave's 16 rows; q_nope
+        // is bf16-valued, so every product is exact in fp32 and the fp64 sums
+        // are exact
+        double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int r = 0; r < kUkRows; ++r) {
             const float q = v[kUkRows * wave + r];
             const uint32_t ww[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                acc[2 * j] = fmaf(q, bf_lo(ww[j]), acc[2 * j]);
-                acc[2 * j + 1] = fmaf(q, bf_hi(ww[j]), acc[2 * j + 1]);
+                acc[2 * j] += (double)(q * bf_lo(ww[j]));
+                acc[2 * j + 1] += (double)(q * bf_hi(ww[j]));
             }
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) part[wave][8 * lane + j] = acc[j];
         __syncthreads();
-        float s = 0.f;
+        double s = 0.0;
 #pragma unroll
         for (int w8 = 0; w8 < kWaves; ++w8) s += part[w8][tid];
-        ws->qc[h][tid] = s;
+        ws->qc[h][tid] = (float)s;
         if (tid < kRope) ws->qpe[h][tid] = rope_one(v + kNope, cs, sn, tid);
         return;
     }
@@ -255,14 +269,14 @@ __global__ __launch_bounds__(kThreads, 1) void prep_kernel(const uint16_t* kv_b,
 // ---------------------------------------------------------------- mla
 // Workgroup (h, k): positions [64 k, min(64 k + 64, pos + 1)). Wave w holds
 // positions 64 k + w + 8 j (j < 8) in registers (lane: c[8 lane .. 8 lane + 7]
-// and k_pe[lane]); scores are fp32 dots times the softmax scale; the partial
-// is (m = max s, l = sum exp(s - m), o = sum exp(s - m) c).
+// and k_pe[lane]). In fp64: the scores s = scale * (q_c . c + q_pe . k_pe),
+// and the chunk partial m = max s, l = sum exp(s - m), o = sum exp(s - m) c.
 __global__ __launch_bounds__(kThreads, 1) void mla_kernel(const uint16_t* cache, Pos P,
-                                                          float scale, Workspace* ws) {
+                                                          double scale, Workspace* ws) {
     __shared__ alignas(16) float qc[kLora];
     __shared__ float qpe[kRope];
-    __shared__ float s[kPosChunk];
-    __shared__ alignas(16) float part[kWaves][kLora];
+    __shared__ double s[kPosChunk];
+    __shared__ double part[kWaves][kLora];
     const int h = blockIdx.x, k = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
     const int pos = read_pos(P);
@@ -282,50 +296,42 @@ __global__ __launch_bounds__(kThreads, 1) void mla_kernel(const uint16_t* cache,
     qc[tid] = ws->qc[h][tid];
     if (tid < kRope) qpe[tid] = ws->qpe[h][tid];
     __syncthreads();
-    float sc[kPerWave];
     const float qp = qpe[lane];
 #pragma unroll
     for (int j = 0; j < kPerWave; ++j) {
-        const uint32_t cw[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
-        float a = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            a = fmaf(bf_lo(cw[q]), qc[8 * lane + 2 * q], a);
-            a = fmaf(bf_hi(cw[q]), qc[8 * lane + 2 * q + 1], a);
+        double a = dot8_xf(c8[j], qc + 8 * lane, 0.0);
+        a += (double)(kp[j] * qp);                             // bf16 x bf16: exact
+        a = wave_sum64(a);
+        if (lane == 0) {
+            const int i = wave + kWaves * j;
+            s[i] = i < n ? a * scale : -INFINITY;
         }
-        sc[j] = fmaf(kp[j], qp, a);
-    }
-    // lane L now holds the wave total of score msum_index<8>(L)
-    const float tot = wave_msum<kPerWave>(sc);
-    {
-        const int i = wave + kWaves * msum_index<kPerWave>(lane);
-        s[i] = i < n ? tot * scale : -INFINITY;                // lanes sharing i write equal values
     }
     __syncthreads();
-    float m = -INFINITY;
-    for (int i = 0; i < n; ++i) m = fmaxf(m, s[i]);
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    double m = -INFINITY;
+    for (int i = 0; i < n; ++i) m = fmax(m, s[i]);
+    double o[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < kPerWave; ++j) {
         const int i = wave + kWaves * j;
-        const float e = i < n ? expf(s[i] - m) : 0.f;
+        const double e = i < n ? exp(s[i] - m) : 0.0;
         const uint32_t cw[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            o[2 * q] = fmaf(e, bf_lo(cw[q]), o[2 * q]);
-            o[2 * q + 1] = fmaf(e, bf_hi(cw[q]), o[2 * q + 1]);
+            o[2 * q] = fma(e, (double)bf_lo(cw[q]), o[2 * q]);
+            o[2 * q + 1] = fma(e, (double)bf_hi(cw[q]), o[2 * q + 1]);
         }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) part[wave][8 * lane + j] = o[j];
     __syncthreads();
-    float acc = 0.f;
+    double acc = 0.0;
 #pragma unroll
     for (int w8 = 0; w8 < kWaves; ++w8) acc += part[w8][tid];
     ws->part_o[h][k][tid] = acc;
     if (tid == 0) {
-        float l = 0.f;
-        for (int i = 0; i < n; ++i) l += expf(s[i] - m);
+        double l = 0.0;
+        for (int i = 0; i < n; ++i) l += exp(s[i] - m);
         ws->part_m[h][k] = m;
         ws->part_l[h][k] = l;
     }
@@ -342,29 +348,22 @@ __global__ __launch_bounds__(kThreads, 1) void combine_kernel(const uint16_t* kv
     const int pos = read_pos(P);
     if (!pos_ok(P, pos)) return;
     const int n_chunks = pos / kPosChunk + 1;
-    float M = -INFINITY;
-    for (int k = 0; k < n_chunks; ++k) M = fmaxf(M, ws->part_m[h][k]);
-    float L = 0.f, o = 0.f;
+    double M = -INFINITY;
+    for (int k = 0; k < n_chunks; ++k) M = fmax(M, ws->part_m[h][k]);
+    double L = 0.0, o = 0.0;
     for (int k = 0; k < n_chunks; ++k) {
-        const float f = expf(ws->part_m[h][k] - M);
-        L = fmaf(f, ws->part_l[h][k], L);
-        o = fmaf(f, ws->part_o[h][k][tid], o);
+        const double f = exp(ws->part_m[h][k] - M);
+        L = fma(f, ws->part_l[h][k], L);
+        o = fma(f, ws->part_o[h][k][tid], o);
     }
-    oc[tid] = o / L;
+    oc[tid] = (float)(o / L);                                 // o_c, rounded once
     __syncthreads();
     const uint16_t* wuv = kv_b + ((int64_t)h * kKvbRowsPerHead + kNope) * kLora;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int dv = 16 * g + 2 * wave + r;
         const u32x4 w8 = reinterpret_cast<const u32x4*>(wuv + (int64_t)dv * kLora)[lane];
-        const uint32_t ww[4] = {w8.x, w8.y, w8.z, w8.w};
-        float a = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            a = fmaf(bf_lo(ww[q]), oc[8 * lane + 2 * q], a);
-            a = fmaf(bf_hi(ww[q]), oc[8 * lane + 2 * q + 1], a);
-        }
-        a = wave_sum(a);
+        const float a = (float)wave_sum64(dot8_xf(w8, oc + 8 * lane, 0.0));
         if (lane == 0) ws->out[h * kV + dv] = (uint16_t)bf16_bits(a);
     }
 }
@@ -507,9 +506,9 @@ extern "C" int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, 
     const int span = pos_dev ? max_pos : pos + 1;
     const int n_chunks = (span + attn::kPosChunk - 1) / attn::kPosChunk;
     // (qk_nope + qk_rope)^-0.5 * mscale(40, 0.707)^2 (src/host/reference_decode.py:
-    // 78-83, 197-203), evaluated in double and rounded once
+    // 78-83, 197-203), in double
     const double m = 0.1 * 0.707 * std::log(40.0) + 1.0;
-    const float scale = (float)(m * m / std::sqrt(192.0));
+    const double scale = std::pow(192.0, -0.5) * m * m;
     hipLaunchKernelGGL(attn::qkv_kernel, dim3(attn::kWG), dim3(attn::kThreads), 0, stream, x,
                        layer->norm_in, layer->qkv, eps, ws);
     hipLaunchKernelGGL(attn::prep_kernel, dim3(attn::kHeads + 1), dim3(attn::kThreads), 0, stream,

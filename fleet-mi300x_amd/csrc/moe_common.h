@@ -77,6 +77,40 @@ __device__ __forceinline__ float dot8_d2(const u32x4& w, const u32x4& x, float a
     return acc;
 }
 
+// Exactly rounded dot products. Every product of two bf16 values is exact in
+// fp32 (8-bit significands), and an fp64 sum of such products is exact as
+// long as the terms span at most 53 bits (for these operands always, up to
+// values far below anything that reaches an fp32 result), so the fp64 total
+// does not depend on the order of the additions and one rounding to fp32
+// gives the correctly rounded fp32 dot product. The decode path evaluates
+// every weight GEMV this way, so its results do not depend on how the rows
+// are split over lanes, waves or workgroups.
+__device__ __forceinline__ double dot8_x(const u32x4& w, const u32x4& x, double acc) {
+    acc += (double)(bf_lo(w.x) * bf_lo(x.x));
+    acc += (double)(bf_hi(w.x) * bf_hi(x.x));
+    acc += (double)(bf_lo(w.y) * bf_lo(x.y));
+    acc += (double)(bf_hi(w.y) * bf_hi(x.y));
+    acc += (double)(bf_lo(w.z) * bf_lo(x.z));
+    acc += (double)(bf_hi(w.z) * bf_hi(x.z));
+    acc += (double)(bf_lo(w.w) * bf_lo(x.w));
+    acc += (double)(bf_hi(w.w) * bf_hi(x.w));
+    return acc;
+}
+
+// bf16 weights against fp32 values (8 + 24 significand bits: the product is
+// exact in fp64 and rounded once into the fp64 sum).
+__device__ __forceinline__ double dot8_xf(const u32x4& w, const float* x, double acc) {
+    acc = fma((double)bf_lo(w.x), (double)x[0], acc);
+    acc = fma((double)bf_hi(w.x), (double)x[1], acc);
+    acc = fma((double)bf_lo(w.y), (double)x[2], acc);
+    acc = fma((double)bf_hi(w.y), (double)x[3], acc);
+    acc = fma((double)bf_lo(w.z), (double)x[4], acc);
+    acc = fma((double)bf_hi(w.z), (double)x[5], acc);
+    acc = fma((double)bf_lo(w.w), (double)x[6], acc);
+    acc = fma((double)bf_hi(w.w), (double)x[7], acc);
+    return acc;
+}
+
 // Same, both operands bf16 chunks.
 __device__ __forceinline__ float dot8_bb(const u32x4& w, const u32x4& h, float acc) {
     acc = fmaf(bf_lo(w.x), bf_lo(h.x), acc);

@@ -319,16 +319,16 @@ __device__ __forceinline__ void finish_pair(const Params& P, int unit, int pair,
                                             const u32x4 (&b)[8], const u32x4 (&xq)[4],
                                             uint32_t tag) {
     const int lane = threadIdx.x & (kLanes - 1);
-    float g = 0.f, u = 0.f;
+    double g = 0.0, u = 0.0;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        g = dot8_d2(b[m], xq[m], g);
-        u = dot8_d2(b[4 + m], xq[m], u);
+        g = dot8_x(b[m], xq[m], g);
+        u = dot8_x(b[4 + m], xq[m], u);
     }
-    g = wave_sum(g);
-    u = wave_sum(u);
+    const float gs = (float)wave_sum64(g);
+    const float us = (float)wave_sum64(u);
     if (lane == 0) {
-        const float h = bf16r(bf16r(silu_rn(bf16r(g))) * bf16r(u));
+        const float h = bf16r(bf16r(silu_rn(bf16r(gs))) * bf16r(us));
         st_agent(&P.ws->h[h_offset(unit) + pair], tag | bf16_bits(h));
     }
 }
@@ -590,11 +590,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         FLEET_TRACE(5);
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            float acc = 0.f;
+            double acc = 0.0;
 #pragma unroll
-            for (int m = 0; m < 3; ++m) acc = dot8_d2(W[3 * r + m], H[m], acc);
-            acc = wave_sum(acc);
-            if (lane == 0) L.part[unit][r] = bf16r(acc);
+            for (int m = 0; m < 3; ++m) acc = dot8_x(W[3 * r + m], H[m], acc);
+            const float d = (float)wave_sum64(acc);
+            if (lane == 0) L.part[unit][r] = bf16r(d);
         }
     } else {
         if (ctl) {
@@ -623,14 +623,14 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const u32x4* wr = reinterpret_cast<const u32x4*>(L.sdown + (rs + r) * kSharedRowBytes);
-            float acc = 0.f;
+            double acc = 0.0;
 #pragma unroll
             for (int m = 0; m < 6; ++m) {
                 const int c = lane + kLanes * m;
-                if (c < kSharedChunks) acc = dot8_d2(wr[c], H[m], acc);
+                if (c < kSharedChunks) acc = dot8_x(wr[c], H[m], acc);
             }
-            acc = wave_sum(acc);
-            if (lane == 0) L.part[0][rs + r] = bf16r(acc);
+            const float d = (float)wave_sum64(acc);
+            if (lane == 0) L.part[0][rs + r] = bf16r(d);
         }
     }
     FLEET_TRACE(6);

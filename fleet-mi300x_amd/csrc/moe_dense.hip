@@ -127,16 +127,16 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     };
     while (cur >= 0) {
         const int nxt = claim();
-        float g = 0.f, u = 0.f;
+        double g = 0.0, u = 0.0;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            g = dot8_d2(buf[m], xq[m], g);
-            u = dot8_d2(buf[4 + m], xq[m], u);
+            g = dot8_x(buf[m], xq[m], g);
+            u = dot8_x(buf[4 + m], xq[m], u);
         }
-        g = wave_sum(g);
-        u = wave_sum(u);
+        const float gs = (float)wave_sum64(g);
+        const float us = (float)wave_sum64(u);
         if (lane == 0) {
-            const float h = bf16r(bf16r(silu_rn(bf16r(g))) * bf16r(u));
+            const float h = bf16r(bf16r(silu_rn(bf16r(gs))) * bf16r(us));
             st_agent(&ws->h[wg + kWG * cur], tag | bf16_bits(h));
         }
         if (nxt >= 0) issue_pair(gu + (int64_t)(wg + kWG * nxt) * 2 * kRowChunks, lane, buf);
@@ -176,15 +176,15 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
         __hip_atomic_fetch_or(&ws->abort, FLEET_MOE_ABORT_UNIT_WAIT, __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    float acc = 0.f;
+    double acc = 0.0;
 #pragma unroll
     for (int i = 0; i < kDnIters; ++i) {
         const int c = lane + kLanes * i;
-        if (c < kDnChunks) acc = dot8_d2(W[i], reinterpret_cast<const u32x4*>(L.hb)[c], acc);
+        if (c < kDnChunks) acc = dot8_x(W[i], reinterpret_cast<const u32x4*>(L.hb)[c], acc);
     }
-    acc = wave_sum(acc);
+    const float d = (float)wave_sum64(acc);
     if (lane == 0) {
-        const float out = bf16r(acc);
+        const float out = bf16r(d);
         P.x_out[n] = bf16r(P.x[n] + out);
         if (P.mlp_out) P.mlp_out[n] = (uint16_t)bf16_bits(out);
     }

@@ -159,7 +159,7 @@ typedef struct fleet_attn_layer {
 } fleet_attn_layer;
 
 /* Workspace bytes fleet_attn_decode, fleet_embed and fleet_lm_head_argmax
- * need (one workspace serves all three; about 2.2 MB). */
+ * need (one workspace serves all three; about 4.3 MB). */
 size_t fleet_attn_workspace_bytes(const fleet_moe_dims* dims);
 
 /* The attention half of one decoder layer at one position:

@@ -23,9 +23,15 @@ OpenBLAS / numpy and is therefore only defined up to a few fp32 ulps):
   deterministic function of the inputs (the GPU path computes them the same
   way, so ids compare bit-exactly);
 * SiLU is evaluated in fp64 and rounded to fp32 before the bf16 rounding;
-* the expert GEMVs accumulate in fp32 (NumPy/OpenBLAS order), exactly as
-  `reference_decode.mlp_unit` does; the GPU accumulates in fp32 in its own
-  order, so expert outputs are compared at bf16 tolerance (rel 1e-2).
+* every other GEMV (expert gate / up / down, the dense MLP, q / kv_a, the
+  absorbed query, W_UV, o_proj, lm_head) is evaluated as each dot product's
+  exact value rounded once to fp32 (`mv_exact`): the value every fp32
+  summation order -- the reference's NumPy/OpenBLAS one included --
+  approximates to within a few fp32 ulps. The attention softmax and its
+  weighted sum of cache rows are evaluated in fp64 and o_c is rounded once.
+  The GPU decode path evaluates them the same way, so its batch-1 outputs
+  compare bit for bit; the multi-token grouped kernel (bf16 MFMA, fp32
+  accumulation) is compared at bf16 tolerance (rel 1e-2).
 
 Parity status of each function (how it is pinned) is listed in
 `tests/test_oracle.py`; every function here is pinned by at least one check
@@ -155,6 +161,30 @@ def route(w_router, x_n, top_k: int = TOP_K, routed_scaling: float = ROUTED_SCAL
     return logits, ids, (pv * np.float32(routed_scaling)).astype(np.float32)
 
 
+# ---------------------------------------------------------------- exact GEMV
+
+def mv_exact(W, x, chunk_elems: int = 1 << 24) -> np.ndarray:
+    """x @ W.T with every dot product's exact value rounded once to fp32.
+
+    W [N, K] (fp32 of bf16 values, or bf16 bits as uint16), x [..., K] (bf16
+    or fp32 values). Products of these operands are exact in fp64 (at most
+    8 + 24 significand bits) and their fp64 sum is exact up to terms 2^53
+    below the largest partial sum, far below what can move an fp32 rounding,
+    so the result does not depend on the summation order. Rows are widened
+    chunk by chunk to bound memory.
+    """
+    W = np.asarray(W)
+    x64 = np.asarray(x, np.float32).astype(np.float64)
+    n, k = W.shape
+    out = np.empty(x64.shape[:-1] + (n,), np.float32)
+    step = max(1, chunk_elems // max(k, 1))
+    for r0 in range(0, n, step):
+        blk = W[r0: r0 + step]
+        blk = bf16_to_f32(blk) if blk.dtype == np.uint16 else blk
+        out[..., r0: r0 + step] = (x64 @ blk.astype(np.float64).T).astype(np.float32)
+    return out
+
+
 # ---------------------------------------------------------------- a5/a6 SwiGLU
 
 def silu(x) -> np.ndarray:
@@ -164,19 +194,19 @@ def silu(x) -> np.ndarray:
 
 
 def swiglu_h(gate, up, x_n) -> np.ndarray:
-    """h = bf16(bf16(silu(bf16(gate x))) * bf16(up x)), fp32 GEMVs.
+    """h = bf16(bf16(silu(bf16(gate x))) * bf16(up x)), exactly rounded GEMVs.
 
     reference_decode.py:263-264 and the epilogue of gemv.h:537-542.
     gate/up: [I, H] fp32 (bf16-valued); x_n: [H] or [T, H].
     """
-    g = bf16_round(np.asarray(x_n, np.float32) @ np.asarray(gate, np.float32).T)
-    u = bf16_round(np.asarray(x_n, np.float32) @ np.asarray(up, np.float32).T)
+    g = bf16_round(mv_exact(gate, x_n))
+    u = bf16_round(mv_exact(up, x_n))
     return bf16_round(bf16_round(silu(g)) * u)
 
 
 def down_proj(down, h) -> np.ndarray:
-    """bf16(down @ h), fp32 GEMV: reference_decode.py:265."""
-    return bf16_round(np.asarray(h, np.float32) @ np.asarray(down, np.float32).T)
+    """bf16(down @ h), exactly rounded GEMV: reference_decode.py:265."""
+    return bf16_round(mv_exact(down, h))
 
 
 def mlp_unit(gate, up, down, x_n) -> np.ndarray:
@@ -516,14 +546,17 @@ class AttnLayer:
 def attention(w: AttnLayer, x, cache, pos: int, cos, sin, eps: float = RMS_EPS) -> dict:
     """Absorbed-MLA decode step (reference_decode.py:210-256), bf16 rounding
     points as there: q and kv_a bf16, c after kv_a_layernorm and k_pe after
-    RoPE bf16 (written to cache[pos]), q_c / scores / softmax / o_c in fp32,
-    the 2048 head outputs bf16, o_proj bf16. cache: fp32 [max_pos][576],
-    rows < pos filled. Returns dict(out, q_c, scores, row)."""
+    RoPE bf16 (written to cache[pos]), q_c fp32, the 2048 head outputs bf16,
+    o_proj bf16. Every GEMV is exactly rounded (mv_exact); the scores, the
+    softmax and its weighted sum of c are evaluated in fp64 and o_c is
+    rounded once to fp32 (the reference's fp32 values, each to within a few
+    ulps). cache: fp32 [max_pos][576], rows < pos filled. Returns dict(out,
+    q_c, scores, row)."""
     H = w.heads
     L, Dk, Dr, Dv = KV_LORA, QK_NOPE, QK_ROPE, V_HEAD
     hidden = np.asarray(x).shape[-1]
     x_n = rms_norm(x, bf16_to_f32(w.norm_in), eps)
-    qkv = bf16_round(w.f32("qkv").reshape(-1, hidden) @ x_n)
+    qkv = bf16_round(mv_exact(w.f32("qkv").reshape(-1, hidden), x_n))
     q = qkv[: H * (Dk + Dr)].reshape(H, Dk + Dr)
     kv_a = qkv[H * (Dk + Dr):]
     c_new = rms_norm(kv_a[:L], bf16_to_f32(w.kv_a_norm), eps)
@@ -531,34 +564,34 @@ def attention(w: AttnLayer, x, cache, pos: int, cos, sin, eps: float = RMS_EPS) 
     q_pe = bf16_round(apply_rope(q[:, Dk:], cos[pos], sin[pos]))
     cache[pos, :L] = c_new
     cache[pos, L:] = k_pe
-    C = cache[: pos + 1, :L]
-    KP = cache[: pos + 1, L:]
+    rows = cache[: pos + 1].astype(np.float64)           # [c ; k_pe] per position
     kv_b = w.f32("kv_b").reshape(H * (Dk + Dv), L)
-    scale = np.float32(softmax_scale())
+    scale = softmax_scale()
     out = np.empty(H * Dv, np.float32)
-    qcs, scs = [], []
+    qcs, scs, ocs = [], [], []
     for h in range(H):
         w_uk = kv_b[h * (Dk + Dv): h * (Dk + Dv) + Dk]
         w_uv = kv_b[h * (Dk + Dv) + Dk: (h + 1) * (Dk + Dv)]
-        q_c = q[h, :Dk] @ w_uk
-        s = (C @ q_c + KP @ q_pe[h]) * scale
-        p = np.exp(s - s.max())
-        p = p / p.sum()
-        out[h * Dv:(h + 1) * Dv] = w_uv @ (p @ C)
+        q_c = mv_exact(w_uk.T, q[h, :Dk])
+        s = (rows @ np.concatenate([q_c, q_pe[h]]).astype(np.float64)) * scale
+        e = np.exp(s - s.max())
+        o_c = ((e @ rows[:, :L]) / e.sum()).astype(np.float32)
+        out[h * Dv:(h + 1) * Dv] = bf16_round(mv_exact(w_uv, o_c))
         qcs.append(q_c)
         scs.append(s)
-    o = bf16_round(w.f32("o_proj").reshape(hidden, H * Dv) @ bf16_round(out))
+        ocs.append(o_c)
+    o = bf16_round(mv_exact(w.f32("o_proj").reshape(hidden, H * Dv), out))
     return {"out": o, "q_c": np.array(qcs), "scores": np.array(scs),
-            "row": cache[pos].copy()}
+            "row": cache[pos].copy(), "qkv": qkv, "o_c": np.array(ocs), "heads": out,
+            "q_pe": q_pe}
 
 
 def lm_head_argmax(x, final_norm, lm_head, eps: float = RMS_EPS) -> dict:
     """Final RMSNorm, logits = bf16(lm_head . x_n) (fleet_kernel.hip:915-920,
-    EPI_BF16), next token = the largest logit, lowest index on ties (the
-    argmax rule of fleet_kernel.hip:509-585)."""
+    EPI_BF16; exactly rounded GEMV), next token = the largest logit, lowest
+    index on ties (the argmax rule of fleet_kernel.hip:509-585)."""
     x_n = rms_norm(x, None if final_norm is None else bf16_to_f32(final_norm), eps)
-    W = lm_head if lm_head.dtype == np.float32 else bf16_to_f32(lm_head)
-    logits = bf16_round(W.reshape(-1, x_n.shape[-1]) @ x_n)
+    logits = bf16_round(mv_exact(np.asarray(lm_head).reshape(-1, x_n.shape[-1]), x_n))
     best = float(logits.max())
     tok = int(np.flatnonzero(logits == best)[0])
     second = float(np.max(np.where(np.arange(logits.size) == tok, -np.inf, logits)))

@@ -236,3 +236,28 @@ def test_lm_head_argmax_matches_oracle():
     torch.cuda.synchronize()
     assert int(tok.item()) == lower
     assert dec.status() == 0
+
+
+def test_rope_bit_exact_over_many_positions(attn_setup):
+    """q_pe and the cached k_pe equal the oracle's three-rounding RoPE
+    (products and sum each rounded to fp32, then bf16) at 400 positions x 16
+    heads: a fused multiply-add in the kernel would move about one element in
+    2^16 (an expected 6 of these 435,200) to the neighbouring bf16 value."""
+    S = attn_setup
+    rng, cos, sin = S["rng"], S["cos"], S["sin"]
+    cache_d = dev16(bits(S["cache"]))
+    dec = ops.AttnDecoder(DSV2_LITE)
+    x = torch.empty(H, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    bad = 0
+    for pos in range(0, MAX_POS, MAX_POS // 400 + 1):
+        x.copy_(torch.from_numpy(_x(rng)))
+        dec.attn_into(S["layer"], x, y, cache_d, pos, None, S["cos_d"], S["sin_d"])
+        g_qkv = ws_f32(dec, WS_QKV, QKV_ROWS)
+        g_qpe = ws_f32(dec, WS_QPE, NH * DR).reshape(NH, DR)
+        g_kpe = orc.bf16_to_f32(cache_d[pos, L:].cpu().numpy().view(np.uint16))
+        q = g_qkv[: NH * (DK + DR)].reshape(NH, DK + DR)
+        bad += int(np.sum(g_qpe != orc.bf16_round(orc.apply_rope(q[:, DK:], cos[pos], sin[pos]))))
+        kv_pe = g_qkv[NH * (DK + DR) + L:]
+        bad += int(np.sum(g_kpe != orc.bf16_round(orc.apply_rope(kv_pe, cos[pos], sin[pos]))))
+    assert bad == 0

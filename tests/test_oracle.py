@@ -433,3 +433,45 @@ def test_moe_bytes_match_model_analysis():
     assert b["shared"] == 34_603_008
     assert b["router"] == 262_144
     assert b["selected"] == 138_412_032
+
+
+def _f32_nearest(q) -> np.float32:
+    """The fp32 nearest to the rational q (ties to even), by exact comparison."""
+    from fractions import Fraction
+    f = np.float32(float(q))
+    lo, hi = np.nextafter(f, np.float32(-np.inf)), np.nextafter(f, np.float32(np.inf))
+    best = min((lo, f, hi), key=lambda c: (abs(Fraction(float(c)) - q),
+                                           int(np.array(c).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def test_mv_exact_is_the_correctly_rounded_dot_product():
+    """mv_exact against exact rational arithmetic: random bf16 rows, bf16 x
+    fp32 rows, and a planted cancellation whose fp32 value depends on the
+    summation order; and within a few fp32 ulps of a plain fp32 product (the
+    reference's NumPy evaluation)."""
+    from fractions import Fraction
+    rng = np.random.default_rng(9)
+    W = orc.bf16_round(0.02 * rng.standard_normal((6, 2048)).astype(np.float32))
+    xb = orc.bf16_round(rng.standard_normal(2048).astype(np.float32))
+    xf = rng.standard_normal(2048).astype(np.float32)
+    for x in (xb, xf):
+        got = orc.mv_exact(W, x)
+        for r in range(W.shape[0]):
+            q = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(W[r], x))
+            assert got[r] == _f32_nearest(q)
+        f32 = (W @ x).astype(np.float32)
+        mag = np.abs(W).astype(np.float64) @ np.abs(x).astype(np.float64)
+        assert np.all(np.abs(f32.astype(np.float64) - got) <= 64 * 2.0 ** -24 * mag)
+    # 1 + 2^-24 + 2^-24 - 1: fp32 left to right loses both small terms, the
+    # exact value is 2^-23
+    w = np.array([[1.0, 2.0 ** -24, 2.0 ** -24, -1.0]], np.float32)
+    x = np.ones(4, np.float32)
+    assert orc.mv_exact(w, x)[0] == np.float32(2.0 ** -23)
+    acc = np.float32(0)
+    for a in w[0]:
+        acc = np.float32(acc + a)
+    assert acc == 0.0
+    # uint16 bf16 bits and batched x give the same values
+    np.testing.assert_array_equal(orc.mv_exact(orc.bf16_bits(W), xb), orc.mv_exact(W, xb))
+    np.testing.assert_array_equal(orc.mv_exact(W, np.stack([xb, xf]))[1], orc.mv_exact(W, xf))
