@@ -13,24 +13,35 @@
 // merged in fp64) and o_c is rounded once to fp32, so no result depends on
 // how positions are split into chunks.
 //
-// One layer is five launches on the caller's stream (each reads what the
-// previous one wrote; the kernel boundary orders them):
-//   qkv      256 workgroups: RMSNorm(x) and the 3648 rows of [q_proj ; kv_a]
-//   prep     17 workgroups: per head q_c = W_UK^T q_nope (8 waves x 16 rows of
-//            W_UK, 1 KB row loads, summed through LDS) and RoPE(q_pe); the 17th
-//            normalises c, rotates k_pe and writes the cache row at pos
-//   mla      16 heads x 64-position chunks: the chunk's 64 scores (a wave per
-//            8 positions, rows held in registers), then its fp64 softmax
-//            partial (max, sum of exp, sum exp * c) from the same registers
-//   combine  16 heads x 8: merge the chunks into o_c, then 16 of the head's 128
-//            outputs of W_UV o_c, bf16
-//   oproj    256 workgroups: 8 rows of o_proj each, bf16, residual add
+// One layer is ONE launch of 256 workgroups (one per CU, 8 waves each) that
+// runs five stages; the data a stage needs from other workgroups crosses as
+// self-validating words (each carries the call's epoch, written and polled
+// with device-scope accesses), so a stage starts as soon as its own inputs
+// are published, and every weight slice and cache row a workgroup will need
+// is put in flight at the start, before the first wait:
+//   S1 qkv    RMSNorm(x) in every workgroup, then the 3648 rows of
+//             [q_proj ; kv_a]: row r in workgroup r % 256, wave (r / 256) % 8.
+//   S2 q_c    workgroup (h, k): columns 32k .. 32k+31 of head h's absorbed
+//             query q_c = W_UK^T q_nope (128 rows x 32 columns of W_UK).
+//   S3 mla    workgroup (h, k): positions chunk k of head h (16 chunks of
+//             ceil((pos+1)/16)): scores, then the chunk's fp64 softmax partial
+//             (max, sum of exp, sum exp * c); the workgroups holding the
+//             current position derive its cache row (kv_a_layernorm of c,
+//             RoPE of k_pe) from kv_a themselves, and (0, k) writes it.
+//   S4 merge  workgroup (h, k): columns 32k .. 32k+31 of o_c merged from the
+//             chunk partials and rounded once; then rows 8k .. 8k+7 of
+//             W_UV o_c, bf16.
+//   S5 oproj  workgroup w: rows 8w .. 8w+7 of o_proj, bf16, residual add.
+// Workgroup w has (h, k) = ((w / 8) % 16, w % 8 + 8 (w / 128)): the 16 heads
+// of one position chunk share an XCD (w % 8), so each XCD's L2 reads its two
+// chunks of the cache once.
 // The position can come from the host (an argument) or from device memory
 // (pos_dev), so a whole decode step can be captured once in a HIP graph and
 // replayed: the argmax kernel then advances *pos_dev itself. A device
 // position outside [0, max_pos) raises FLEET_MOE_ABORT_POSITION and the layer
 // does nothing past the check; a token outside the vocabulary raises
-// FLEET_MOE_ABORT_TOKEN in the embedding, which then writes zeros.
+// FLEET_MOE_ABORT_TOKEN in the embedding, which then writes zeros. Every
+// cross-workgroup wait is bounded (FLEET_MOE_ABORT_ATTN_WAIT).
 //
 // Cache layout [max_pos][512 + 64] bf16 per layer: c after kv_a_layernorm,
 // then k_pe after RoPE in DeepseekV2's reordered basis. RoPE tables (cos, sin
@@ -53,43 +64,49 @@ constexpr int kQDim = kHeads * (kNope + kRope);          // 3072
 constexpr int kQkvRows = kQDim + kLora + kRope;          // 3648
 constexpr int kKvbRowsPerHead = kNope + kV;              // 256
 constexpr int kRowElems = kLora + kRope;                 // 576: one cache row
-constexpr int kPosChunk = 64;                            // positions per mla workgroup
 constexpr int kMaxPos = 4096;
-constexpr int kMaxChunks = kMaxPos / kPosChunk;          // 64
 constexpr int kVocab = 102400;
 constexpr int kWG = 256;
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kLanes;
-constexpr int kPerWave = kPosChunk / kWaves;             // 8 positions per wave in mla
-constexpr int kUkRows = kNope / kWaves;                  // 16 W_UK rows per wave in prep
+constexpr int kChunks = kWG / kHeads;                    // 16 position chunks per head
+constexpr int kQcCols = kLora / kChunks;                 // 32 columns of q_c / o_c per workgroup
+constexpr int kUkRows = kNope / kWaves;                  // 16 W_UK rows per wave
+constexpr int kUvRows = kV / kChunks;                    // 8 W_UV rows per workgroup
+constexpr int kOpRows = kHidden / kWG;                   // 8 o_proj rows per workgroup
+constexpr int kBatch = 12;                               // cache rows a wave holds at once
+static_assert(kHeads * kChunks == kWG && kQcCols * kChunks == kLora, "work split");
+static_assert(kUvRows == kWaves && kOpRows == kWaves, "one row per wave in the epilogues");
+static_assert(kBatch <= kLanes, "one lane per row for the exponentials");
 
 struct Workspace {
-    uint32_t epoch;                            // unused by these kernels
-    uint32_t pad0;
+    uint32_t epoch;                            // calls completed on this workspace
+    uint32_t exits;                            // workgroup exits over all calls
     uint32_t abort;                            // offset 8: sticky status
     uint32_t pad1[61];
-    float qkv[kQkvRows];                       // bf16-valued
-    float qc[kHeads][kLora];                   // absorbed queries
-    float qpe[kHeads][kRope];                  // rotated, bf16-valued
-    double part_m[kHeads][kMaxChunks];         // chunk partials of the softmax, fp64
-    double part_l[kHeads][kMaxChunks];
-    double part_o[kHeads][kMaxChunks][kLora];
-    uint16_t out[kHeads * kV];                 // bf16 head outputs
+    float qkv[kQkvRows];                       // plain copies of the published values
+    float qc[kHeads][kLora];
+    float qpe[kHeads][kRope];
+    // Published values. Every 32-bit word is (epoch & 0xffff) << 16 | 16
+    // payload bits: a bf16 in one word, an fp32 in two (high half first), an
+    // fp64 in four, so a word read with any tearing of wider accesses still
+    // proves its own freshness.
+    uint32_t qkv_t[kQkvRows];                  // bf16 q / kv_a
+    uint32_t qc_t[kHeads][kLora][2];           // fp32 q_c
+    uint32_t ml_t[kHeads][kChunks][8];         // fp64 chunk max, then fp64 chunk sum of exp
+    uint32_t o_t[kHeads][kChunks][kLora][4];   // fp64 chunk sum of exp * c
+    uint32_t oc_t[kHeads][kLora][2];           // fp32 o_c
+    uint32_t out_t[kHeads * kV];               // bf16 head outputs
     float cand_v[kWG];                         // lm_head: best logit per workgroup
     int32_t cand_i[kWG];
 };
 static_assert(offsetof(Workspace, abort) == 8, "status word offset");
-static_assert(offsetof(Workspace, qkv) % 16 == 0, "16-byte aligned arrays");
-static_assert(offsetof(Workspace, out) % 16 == 0, "head outputs are read with 16-byte loads");
-
-struct Pos {
-    const int32_t* dev;   // device position, or null: use `host`
-    int32_t host;
-    int32_t max_pos;
-};
-
-__device__ __forceinline__ int read_pos(const Pos& p) { return p.dev ? *p.dev : p.host; }
-__device__ __forceinline__ bool pos_ok(const Pos& p, int pos) { return pos >= 0 && pos < p.max_pos; }
+static_assert(offsetof(Workspace, qkv) == 256, "plain copies follow the header");
+static_assert(offsetof(Workspace, qkv_t) % 16 == 0 && offsetof(Workspace, qc_t) % 16 == 0 &&
+                  offsetof(Workspace, ml_t) % 16 == 0 && offsetof(Workspace, o_t) % 16 == 0 &&
+                  offsetof(Workspace, oc_t) % 16 == 0 && offsetof(Workspace, out_t) % 16 == 0,
+              "polled arrays are read with 16-byte loads");
+static_assert(sizeof(Workspace) < (1u << 31), "32-bit buffer offsets");
 
 __device__ __forceinline__ void raise(Workspace* ws, uint32_t bit) {
     __hip_atomic_fetch_or(&ws->abort, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -98,12 +115,8 @@ __device__ __forceinline__ void raise(Workspace* ws, uint32_t bit) {
 // RMSNorm of a 2048-vector held 4 per thread (512 threads), the arithmetic of
 // the MoE decode kernel (fp64 sum of squares, correctly rounded sqrt and
 // division, two bf16 roundings); writes the bf16 result as packed pairs.
-__device__ void norm2048(const float* x, const uint16_t* gamma, float eps, uint32_t* xb,
-                         double* red) {
+__device__ void norm2048(const float4 xv, const uint2 gb, float eps, uint32_t* xb, double* red) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
-    const float4 xv = reinterpret_cast<const float4*>(x)[tid];
-    const uint2 gb = gamma ? reinterpret_cast<const uint2*>(gamma)[tid]
-                           : make_uint2(0x3f803f80u, 0x3f803f80u);
     double ss = (double)xv.x * xv.x + (double)xv.y * xv.y + (double)xv.z * xv.z +
                 (double)xv.w * xv.w;
     ss = wave_sum64(ss);
@@ -139,40 +152,21 @@ __device__ __forceinline__ float dot_row(const u32x4 (&w)[4], const u32x4 (&xq)[
     return (float)wave_sum64(a);
 }
 
-// Rows first, first + stride, ... (< end) of a K = 2048 matrix against the
-// packed bf16 vector xq; each wave keeps its next row in flight while it
-// reduces the current one. f(row, value) receives every wave total.
-template <typename F>
-__device__ __forceinline__ void gemv_rows2048(const uint16_t* W, int first, int stride, int end,
-                                              const u32x4 (&xq)[4], F f) {
-    if (first >= end) return;
-    u32x4 w[4], wn[4];
-    load_row(W, first, w);
-    for (int row = first; row < end; row += stride) {
-        const int nxt = row + stride;
-        if (nxt < end) load_row(W, nxt, wn);
-        f(row, dot_row(w, xq));
-#pragma unroll
-        for (int m = 0; m < 4; ++m) w[m] = wn[m];
-    }
+// Sum over the 8 lanes of each aligned group of 8 (quad exchanges, then the
+// half-row mirror); every lane of the group returns the group total.
+__device__ __forceinline__ double sum8_lanes(double v) {
+    v += dpp64<0xB1>(v);
+    v += dpp64<0x4E>(v);
+    v += dpp64<0x141>(v);
+    return v;
 }
 
-// ---------------------------------------------------------------- qkv
-// Row r of [q_proj ; kv_a] goes to workgroup r % 256, wave (r / 256) % 8.
-__global__ __launch_bounds__(kThreads, 1) void qkv_kernel(const float* x, const uint16_t* norm,
-                                                          const uint16_t* W, float eps,
-                                                          Workspace* ws) {
-    __shared__ alignas(16) uint32_t xb[kHidden / 2];
-    __shared__ double red[kWaves];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    norm2048(x, norm, eps, xb, red);
-    u32x4 xq[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(xb)[lane + kLanes * m];
-    gemv_rows2048(W, blockIdx.x + kWG * wave, kWG * kWaves, kQkvRows, xq,
-                  [&](int row, float a) {
-                      if (lane == 0) ws->qkv[row] = bf16r(a);
-                  });
+__device__ __forceinline__ double wave_max64(double v) {
+    v = fmax(v, dpp64<0xB1>(v));
+    v = fmax(v, dpp64<0x4E>(v));
+    v = fmax(v, dpp64<0x141>(v));
+    v = fmax(v, dpp64<0x140>(v));
+    return fmax(fmax(readlane64(v, 0), readlane64(v, 16)), fmax(readlane64(v, 32), readlane64(v, 48)));
 }
 
 // DeepseekV2 RoPE of 64 bf16-valued inputs v: reordered basis y = [v0, v2, ..,
@@ -193,195 +187,487 @@ __device__ __forceinline__ float rope_one(const float* v, const float* cs, const
     return bf16r(a + b);
 }
 
-// ---------------------------------------------------------------- prep
-// blockIdx.x < 16: head h's absorbed query and rotated q_pe;
-// blockIdx.x == 16: the new cache row.
-__global__ __launch_bounds__(kThreads, 1) void prep_kernel(const uint16_t* kv_b,
-                                                           const uint16_t* kv_a_norm,
-                                                           const float* rope_cos,
-                                                           const float* rope_sin, Pos P,
-                                                           uint16_t* cache, float eps,
-                                                           Workspace* ws) {
-    __shared__ float v[kLora + kRope];
-    __shared__ double part[kWaves][kLora];
-    __shared__ double red[kWaves];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
-    const int pos = read_pos(P);
-    if (!pos_ok(P, pos)) {
-        if (blockIdx.x == kHeads && tid == 0) raise(ws, FLEET_MOE_ABORT_POSITION);
+// ---------------------------------------------------------------- polling
+// A 16-byte group of published words is complete when each of its four
+// 32-bit words carries this call's 16-bit tag.
+__device__ __forceinline__ bool tagged(const u32x4& v, uint32_t tag) {
+    return ((v.x & 0xffff0000u) == tag) & ((v.y & 0xffff0000u) == tag) &
+           ((v.z & 0xffff0000u) == tag) & ((v.w & 0xffff0000u) == tag);
+}
+
+// Polls (device-scope 16-byte loads, a short sleep between rounds) until the
+// group at byte offset `off` of `base` carries `tag` in every active lane.
+// Called by whole waves; lanes with `active` false load nothing. A wait that
+// runs out (or finds the sticky status set by another wait) raises
+// FLEET_MOE_ABORT_ATTN_WAIT and returns false; the caller carries on with
+// whatever was read, so the grid always drains.
+__device__ bool poll16(const void* base, int off, bool active, uint32_t tag, u32x4& v,
+                       Workspace* ws) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(base);
+    for (uint32_t it = 0;; ++it) {
+        v = active ? ld_dev16(r, off) : u32x4{0u, 0u, 0u, 0u};
+        if (__all(!active || tagged(v, tag))) return true;
+        if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&ws->abort) != 0)) {
+            if ((threadIdx.x & (kLanes - 1)) == 0) raise(ws, FLEET_MOE_ABORT_ATTN_WAIT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Payload of tagged words: an fp64 from four words, an fp32 from two.
+__device__ __forceinline__ double tagged_f64(const u32x4& v) {
+    const uint64_t b = ((uint64_t)(v.x & 0xffffu) << 48) | ((uint64_t)(v.y & 0xffffu) << 32) |
+                       ((v.z & 0xffffu) << 16) | (v.w & 0xffffu);
+    return __longlong_as_double((long long)b);
+}
+__device__ __forceinline__ float tagged_f32(uint32_t hi, uint32_t lo) {
+    return __uint_as_float((hi << 16) | (lo & 0xffffu));
+}
+// Two tagged words (high payload half at the lower address) as one 64-bit
+// device-scope store.
+__device__ __forceinline__ void publish_pair(uint32_t* p, uint32_t bits, uint32_t tag) {
+    const uint64_t w = ((uint64_t)(tag | (bits & 0xffffu)) << 32) | (tag | (bits >> 16));
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_f32(uint32_t* p, float f, uint32_t tag) {
+    publish_pair(p, __float_as_uint(f), tag);
+}
+__device__ __forceinline__ void publish_f64(uint32_t* p, double d, uint32_t tag) {
+    const uint64_t b = (uint64_t)__double_as_longlong(d);
+    publish_pair(p, (uint32_t)(b >> 32), tag);
+    publish_pair(p + 2, (uint32_t)b, tag);
+}
+
+// ---------------------------------------------------------------- the layer kernel
+struct Params {
+    const float* x;
+    float* x_out;
+    const uint16_t* norm_in;
+    const uint16_t* qkv;
+    const uint16_t* kv_a_norm;
+    const uint16_t* kv_b;
+    const uint16_t* o_proj;
+    uint16_t* cache;
+    const float* cos;
+    const float* sin;
+    const int32_t* pos_dev;
+    int32_t pos_host;
+    int32_t max_pos;
+    double scale;
+    float eps;
+    Workspace* ws;
+};
+
+struct Lds {
+    alignas(16) uint32_t xb[kHidden / 2];      // x_norm as bf16 pairs
+    double red[kWaves];
+    union {
+        struct {                                // S2
+            double uk[kWaves][kUkRows][kQcCols];
+            double uk2[kUkRows][kQcCols];
+        } s2;
+        struct {                                // S3
+            alignas(16) float qc[kLora];
+            float qpe_raw[kRope];
+            float qpe[kRope];
+            float kva[kLora + kRope];
+            alignas(16) uint16_t row[kRowElems];    // the cache row of the current position
+            double wm[kWaves], wl[kWaves], wf[kWaves];
+            double wo[kWaves][kLora];
+        } s3;
+        struct {                                // S4
+            double mo[kChunks][kQcCols];
+            double mm[kChunks], ml[kChunks], f[kChunks];
+            alignas(16) float oc[kLora];
+            double uvr[kWaves][kUvRows];
+        } s4;
+        struct {                                // S5
+            alignas(16) uint16_t outv[kHeads * kV];
+            double opr[kWaves][kOpRows];
+        } s5;
+    } u;
+};
+
+__global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
+    __shared__ Lds L;
+    const int wg = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
+    Workspace* ws = P.ws;
+    const int pos = P.pos_dev ? *P.pos_dev : P.pos_host;
+    if (pos < 0 || pos >= P.max_pos) {
+        if (wg == 0 && tid == 0) raise(ws, FLEET_MOE_ABORT_POSITION);
         return;
     }
-    const float* cs = rope_cos + (int64_t)pos * kRope;
-    const float* sn = rope_sin + (int64_t)pos * kRope;
-    if (blockIdx.x < kHeads) {
-        const int h = blockIdx.x;
-        const u32x4* wuk = reinterpret_cast<const u32x4*>(kv_b + (int64_t)h * kKvbRowsPerHead * kLora);
-        u32x4 w[kUkRows];
+    const int h = (wg >> 3) & (kHeads - 1);
+    const int k = (wg & 7) + 8 * (wg >> 7);
+    const int n_pos = pos + 1;
+    const int C = (n_pos + kChunks - 1) / kChunks;      // positions per chunk
+    const int n_used = (n_pos + C - 1) / C;             // chunks holding positions
+    const int t0 = k * C;
+    const int t1 = min(t0 + C, n_pos);
+    const bool has_rows = k < n_used;
+    const bool last = k == n_used - 1;                  // the chunk holding `pos`
+
+    // ---- everything this workgroup will read, in order of need
+    const uint32_t epoch = ld_agent(&ws->epoch) + 1u;
+    const uint32_t tag = (epoch & 0xffffu) << 16;
+    const float4 xv = reinterpret_cast<const float4*>(P.x)[tid];
+    const uint2 gb = P.norm_in ? reinterpret_cast<const uint2*>(P.norm_in)[tid]
+                               : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
+    const float x_own = tid < kOpRows ? P.x[kOpRows * wg + tid] : 0.f;
+    const int r0 = wg + kWG * wave;                       // < 2048
+    const int r1 = wg + kWG * (wave + kWaves);            // valid below 3648
+    u32x4 wq0[4], wq1[4];
+    load_row(P.qkv, r0, wq0);
+    if (r1 < kQkvRows) load_row(P.qkv, r1, wq1);
+    // W_UK of head h: row 16 wave + lane / 4, columns 32 k + 8 (lane % 4) .. + 7
+    const u32x4 wuk = ld_stream(reinterpret_cast<const u32x4*>(
+        P.kv_b + ((int64_t)h * kKvbRowsPerHead + kUkRows * wave + (lane >> 2)) * kLora +
+        kQcCols * k + 8 * (lane & 3)));
+    // this wave's first cache rows of the chunk (rows before `pos`; row `pos`
+    // is derived from kv_a below)
+    u32x4 c8[kBatch];
+    float kp[kBatch];
+    const int t_end = min(t1, pos);
 #pragma unroll
-        for (int r = 0; r < kUkRows; ++r)
-            w[r] = ld_stream(wuk + (int64_t)(kUkRows * wave + r) * (kLora / kChunk) + lane);
-        if (tid < kNope + kRope) v[tid] = ws->qkv[h * (kNope + kRope) + tid];
-        __syncthreads();
-        // lane holds columns 8 lane .. 8 lane + 7 of this wave's 16 rows; q_nope
-        // is bf16-valued, so every product is exact in fp32 and the fp64 sums
-        // are exact
-        double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    for (int i = 0; i < kBatch; ++i) {
+        const int t = t0 + wave + kWaves * i;
+        if (t < t_end) {
+            const uint16_t* row = P.cache + (int64_t)t * kRowElems;
+            c8[i] = reinterpret_cast<const u32x4*>(row)[lane];
+            kp[i] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
+        } else {
+            c8[i] = u32x4{0u, 0u, 0u, 0u};
+            kp[i] = 0.f;
+        }
+    }
+    // W_UV of head h: row 8 k + lane / 8, columns 64 wave + 8 (lane % 8) .. + 7
+    const u32x4 wuv = ld_stream(reinterpret_cast<const u32x4*>(
+        P.kv_b + ((int64_t)h * kKvbRowsPerHead + kNope + kUvRows * k + (lane >> 3)) * kLora +
+        64 * wave + 8 * (lane & 7)));
+    // o_proj: row 8 wg + lane / 8, columns 256 wave + 32 (lane % 8) .. + 31
+    u32x4 wo[4];
+    {
+        const u32x4* p = reinterpret_cast<const u32x4*>(
+            P.o_proj + (int64_t)(kOpRows * wg + (lane >> 3)) * kHidden + 256 * wave +
+            32 * (lane & 7));
 #pragma unroll
-        for (int r = 0; r < kUkRows; ++r) {
-            const float q = v[kUkRows * wave + r];
-            const uint32_t ww[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+        for (int m = 0; m < 4; ++m) wo[m] = ld_stream(p + m);
+    }
+
+    // ---- S1: RMSNorm, then this wave's rows of [q_proj ; kv_a]
+    norm2048(xv, gb, P.eps, L.xb, L.red);
+    {
+        u32x4 xq[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[2 * j] += (double)(q * bf_lo(ww[j]));
-                acc[2 * j + 1] += (double)(q * bf_hi(ww[j]));
+        for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
+        const float a0 = bf16r(dot_row(wq0, xq));
+        if (lane == 0) {
+            ws->qkv[r0] = a0;
+            st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
+        }
+        if (r1 < kQkvRows) {
+            const float a1 = bf16r(dot_row(wq1, xq));
+            if (lane == 0) {
+                ws->qkv[r1] = a1;
+                st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
             }
         }
+    }
+
+    // ---- S2: q_c[h][32k .. 32k+31] = sum over the 128 rows of W_UK q_nope
+    {
+        u32x4 qn;
+        poll16(ws->qkv_t, 4 * (h * (kNope + kRope) + kUkRows * wave) + 16 * lane, lane < 4,
+               tag, qn, ws);
+        // lane needs q_nope[16 wave + lane / 4]: word (lane / 4) % 4 of lane lane / 16
+        const int src = (lane >> 4) << 2;
+        const uint32_t c0 = __builtin_amdgcn_ds_bpermute(src, qn.x);
+        const uint32_t c1 = __builtin_amdgcn_ds_bpermute(src, qn.y);
+        const uint32_t c2 = __builtin_amdgcn_ds_bpermute(src, qn.z);
+        const uint32_t c3 = __builtin_amdgcn_ds_bpermute(src, qn.w);
+        const int comp = (lane >> 2) & 3;
+        const uint32_t wd = comp == 0 ? c0 : comp == 1 ? c1 : comp == 2 ? c2 : c3;
+        const float q = __uint_as_float(wd << 16);
+        // bf16 x bf16 products are exact in fp32, so every sum below is exact
+        const uint32_t ww[4] = {wuk.x, wuk.y, wuk.z, wuk.w};
+        double* dst = &L.u.s2.uk[wave][lane >> 2][8 * (lane & 3)];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) part[wave][8 * lane + j] = acc[j];
+        for (int jj = 0; jj < 4; ++jj) {
+            dst[2 * jj] = (double)(q * bf_lo(ww[jj]));
+            dst[2 * jj + 1] = (double)(q * bf_hi(ww[jj]));
+        }
         __syncthreads();
-        double s = 0.0;
+        {
+            const int col = tid & (kQcCols - 1), part = tid >> 5;
+            double s = 0.0;
 #pragma unroll
-        for (int w8 = 0; w8 < kWaves; ++w8) s += part[w8][tid];
-        ws->qc[h][tid] = (float)s;
-        if (tid < kRope) ws->qpe[h][tid] = rope_one(v + kNope, cs, sn, tid);
-        return;
+            for (int w = 0; w < kWaves; ++w) s += L.u.s2.uk[w][part][col];
+            L.u.s2.uk2[part][col] = s;
+        }
+        __syncthreads();
+        if (tid < kQcCols) {
+            double s = 0.0;
+#pragma unroll
+            for (int p = 0; p < kUkRows; ++p) s += L.u.s2.uk2[p][tid];
+            const float qc = (float)s;
+            ws->qc[h][kQcCols * k + tid] = qc;
+            publish_f32(ws->qc_t[h][kQcCols * k + tid], qc, tag);
+        }
+        __syncthreads();
     }
-    // c = rms_norm(kv_a[:512], kv_a_norm) (two bf16 roundings), k_pe = RoPE(kv_a[512:])
-    const float* kva = ws->qkv + kQDim;
-    const float c = kva[tid];
-    double ss = (double)c * c;
-    ss = wave_sum64(ss);
-    if (lane == 0) red[wave] = ss;
-    if (tid < kRope) v[tid] = kva[kLora + tid];
-    __syncthreads();
-    double ssq = 0.0;
-#pragma unroll
-    for (int w8 = 0; w8 < kWaves; ++w8) ssq += red[w8];
-    const float var = (float)(ssq / (double)kLora);
-    const float inv = __fdiv_rn(1.0f, sqrt_rn(var + eps));
-    const float g = kv_a_norm ? __uint_as_float((uint32_t)kv_a_norm[tid] << 16) : 1.0f;
-    const float cn = bf16r(bf16r(c * inv) * g);
-    uint16_t* row = cache + (int64_t)pos * kRowElems;
-    row[tid] = (uint16_t)bf16_bits(cn);
-    if (tid < kRope) row[kLora + tid] = (uint16_t)bf16_bits(rope_one(v, cs, sn, tid));
-}
 
-// ---------------------------------------------------------------- mla
-// Workgroup (h, k): positions [64 k, min(64 k + 64, pos + 1)). Wave w holds
-// positions 64 k + w + 8 j (j < 8) in registers (lane: c[8 lane .. 8 lane + 7]
-// and k_pe[lane]). In fp64: the scores s = scale * (q_c . c + q_pe . k_pe),
-// and the chunk partial m = max s, l = sum exp(s - m), o = sum exp(s - m) c.
-__global__ __launch_bounds__(kThreads, 1) void mla_kernel(const uint16_t* cache, Pos P,
-                                                          double scale, Workspace* ws) {
-    __shared__ alignas(16) float qc[kLora];
-    __shared__ float qpe[kRope];
-    __shared__ double s[kPosChunk];
-    __shared__ double part[kWaves][kLora];
-    const int h = blockIdx.x, k = blockIdx.y;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
-    const int pos = read_pos(P);
-    if (!pos_ok(P, pos)) return;
-    const int t0 = k * kPosChunk;
-    if (t0 > pos) return;
-    const int n = min(kPosChunk, pos + 1 - t0);
-    u32x4 c8[kPerWave];
-    float kp[kPerWave];
+    // ---- S3: the chunk's scores and fp64 softmax partial
+    const float* cs = P.cos + (int64_t)pos * kRope;
+    const float* sn = P.sin + (int64_t)pos * kRope;
+    if (has_rows) {
+        u32x4 v;
+        if (wave < 4) {
+            // q_c of head h: 512 tagged words, 2 per lane
+            poll16(ws->qc_t, 8 * (h * kLora + 128 * wave + 2 * lane), true, tag, v, ws);
+            L.u.s3.qc[128 * wave + 2 * lane] = tagged_f32(v.x, v.y);
+            L.u.s3.qc[128 * wave + 2 * lane + 1] = tagged_f32(v.z, v.w);
+        } else if (wave == 4) {
+            // q_pe of head h before RoPE: 64 words, 4 per lane
+            poll16(ws->qkv_t, 4 * (h * (kNope + kRope) + kNope) + 16 * lane, lane < 16,
+                   tag, v, ws);
+            if (lane < 16) {
+                L.u.s3.qpe_raw[4 * lane] = __uint_as_float(v.x << 16);
+                L.u.s3.qpe_raw[4 * lane + 1] = __uint_as_float(v.y << 16);
+                L.u.s3.qpe_raw[4 * lane + 2] = __uint_as_float(v.z << 16);
+                L.u.s3.qpe_raw[4 * lane + 3] = __uint_as_float(v.w << 16);
+            }
+        } else if (last) {
+            // kv_a (576 words): waves 5, 6, 7 take words 0..255, 256..511, 512..575
+            const int w0 = 256 * (wave - 5);
+            const bool act = w0 + 4 * lane < kLora + kRope;
+            poll16(ws->qkv_t, 4 * (kQDim + w0) + 16 * lane, act, tag, v, ws);
+            if (act) {
+                L.u.s3.kva[w0 + 4 * lane] = __uint_as_float(v.x << 16);
+                L.u.s3.kva[w0 + 4 * lane + 1] = __uint_as_float(v.y << 16);
+                L.u.s3.kva[w0 + 4 * lane + 2] = __uint_as_float(v.z << 16);
+                L.u.s3.kva[w0 + 4 * lane + 3] = __uint_as_float(v.w << 16);
+            }
+        }
+        __syncthreads();
+        if (tid < kRope) {
+            const float qp = rope_one(L.u.s3.qpe_raw, cs, sn, tid);
+            L.u.s3.qpe[tid] = qp;
+            if (k == 0) ws->qpe[h][tid] = qp;
+        }
+        if (last) {
+            // c = kv_a_layernorm(kv_a[:512]) (two bf16 roundings), k_pe = RoPE(kv_a[512:])
+            const float c = L.u.s3.kva[tid];
+            const double ss = wave_sum64((double)c * c);
+            if (lane == 0) L.red[wave] = ss;
+            __syncthreads();
+            double ssq = 0.0;
 #pragma unroll
-    for (int j = 0; j < kPerWave; ++j) {
-        const int i = min(wave + kWaves * j, n - 1);          // clamped: always a written row
-        const uint16_t* row = cache + (int64_t)(t0 + i) * kRowElems;
-        c8[j] = reinterpret_cast<const u32x4*>(row)[lane];
-        kp[j] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
-    }
-    qc[tid] = ws->qc[h][tid];
-    if (tid < kRope) qpe[tid] = ws->qpe[h][tid];
-    __syncthreads();
-    const float qp = qpe[lane];
+            for (int w = 0; w < kWaves; ++w) ssq += L.red[w];
+            const float var = (float)(ssq / (double)kLora);
+            const float inv = __fdiv_rn(1.0f, sqrt_rn(var + P.eps));
+            const float g = P.kv_a_norm ? __uint_as_float((uint32_t)P.kv_a_norm[tid] << 16) : 1.0f;
+            const uint16_t cb = (uint16_t)bf16_bits(bf16r(bf16r(c * inv) * g));
+            L.u.s3.row[tid] = cb;
+            uint16_t kb = 0;
+            if (tid < kRope) {
+                kb = (uint16_t)bf16_bits(rope_one(L.u.s3.kva + kLora, cs, sn, tid));
+                L.u.s3.row[kLora + tid] = kb;
+            }
+            if (h == 0) {
+                uint16_t* crow = P.cache + (int64_t)pos * kRowElems;
+                crow[tid] = cb;
+                if (tid < kRope) crow[kLora + tid] = kb;
+            }
+        }
+        __syncthreads();
+
+        float qcl[8];
 #pragma unroll
-    for (int j = 0; j < kPerWave; ++j) {
-        double a = dot8_xf(c8[j], qc + 8 * lane, 0.0);
-        a += (double)(kp[j] * qp);                             // bf16 x bf16: exact
-        a = wave_sum64(a);
+        for (int jj = 0; jj < 8; ++jj) qcl[jj] = L.u.s3.qc[8 * lane + jj];
+        const float qp = L.u.s3.qpe[lane];
+        const u32x4 rc = reinterpret_cast<const u32x4*>(L.u.s3.row)[lane];
+        const float rk = __uint_as_float((uint32_t)L.u.s3.row[kLora + lane] << 16);
+        double m_w = -INFINITY, l_w = 0.0;
+        double o[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+        for (int base = t0 + wave, b = 0; base < t1; base += kWaves * kBatch, ++b) {
+            if (b > 0) {
+#pragma unroll
+                for (int i = 0; i < kBatch; ++i) {
+                    const int t = base + kWaves * i;
+                    if (t < t_end) {
+                        const uint16_t* row = P.cache + (int64_t)t * kRowElems;
+                        c8[i] = reinterpret_cast<const u32x4*>(row)[lane];
+                        kp[i] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
+                    }
+                }
+            }
+            double s[kBatch];
+            double mb = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                const int t = base + kWaves * i;
+                s[i] = -INFINITY;
+                if (t < t1) {
+                    const bool cur = t == pos;
+                    const u32x4 cv = cur ? rc : c8[i];
+                    const float kv = cur ? rk : kp[i];
+                    double a = dot8_xf(cv, qcl, 0.0);
+                    a += (double)(kv * qp);                    // bf16 x bf16: exact
+                    s[i] = wave_sum64(a) * P.scale;
+                    mb = fmax(mb, s[i]);
+                }
+            }
+            const double m_new = fmax(m_w, mb);
+            const double fo = exp(m_w - m_new);            // 0 while nothing is accumulated
+            double sv = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) sv = lane == i ? s[i] : sv;
+            const double ev = exp(sv - m_new);             // one row per lane; exp(-inf) = 0
+            l_w *= fo;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) o[jj] *= fo;
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                const int t = base + kWaves * i;
+                if (t < t1) {
+                    const double e = readlane64(ev, i);
+                    const u32x4 cv = t == pos ? rc : c8[i];
+                    const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+                    l_w += e;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        o[2 * q] = fma(e, (double)bf_lo(cw[q]), o[2 * q]);
+                        o[2 * q + 1] = fma(e, (double)bf_hi(cw[q]), o[2 * q + 1]);
+                    }
+                }
+            }
+            m_w = m_new;
+        }
         if (lane == 0) {
-            const int i = wave + kWaves * j;
-            s[i] = i < n ? a * scale : -INFINITY;
+            L.u.s3.wm[wave] = m_w;
+            L.u.s3.wl[wave] = l_w;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) L.u.s3.wo[wave][8 * lane + jj] = o[jj];
+        __syncthreads();
+        double M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmax(M, L.u.s3.wm[w]);
+        if (tid < kWaves) L.u.s3.wf[tid] = exp(L.u.s3.wm[tid] - M);
+        __syncthreads();
+        double O = 0.0, Ls = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            O = fma(L.u.s3.wf[w], L.u.s3.wo[w][tid], O);
+            Ls = fma(L.u.s3.wf[w], L.u.s3.wl[w], Ls);
+        }
+        publish_f64(ws->o_t[h][k][tid], O, tag);
+        if (tid == 0) {
+            publish_f64(&ws->ml_t[h][k][0], M, tag);
+            publish_f64(&ws->ml_t[h][k][4], Ls, tag);
         }
     }
     __syncthreads();
-    double m = -INFINITY;
-    for (int i = 0; i < n; ++i) m = fmax(m, s[i]);
-    double o[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+
+    // ---- S4: o_c[h][32k .. 32k+31] from the chunk partials, then W_UV rows 8k .. 8k+7
+    {
+        // wave w: chunks 2w and 2w + 1 (column 32k + lane % 32), and their max / sum
+        const int c = 2 * wave + (lane >> 5);
+        u32x4 v;
+        poll16(ws->o_t, (int)(((h * kChunks + c) * kLora + kQcCols * k + (lane & 31)) * 16),
+               c < n_used, tag, v, ws);
+        if (c < n_used) L.u.s4.mo[c][lane & 31] = tagged_f64(v);
+        const int cm = 2 * wave + (lane >> 1);
+        poll16(ws->ml_t, (int)(((h * kChunks + cm) * 8 + 4 * (lane & 1)) * 4),
+               lane < 4 && cm < n_used, tag, v, ws);
+        if (lane < 4 && cm < n_used) {
+            if (lane & 1) L.u.s4.ml[cm] = tagged_f64(v);
+            else L.u.s4.mm[cm] = tagged_f64(v);
+        }
+        __syncthreads();
+        if (tid < kChunks) {
+            double M = -INFINITY;
+            for (int q = 0; q < n_used; ++q) M = fmax(M, L.u.s4.mm[q]);
+            L.u.s4.f[tid] = tid < n_used ? exp(L.u.s4.mm[tid] - M) : 0.0;
+        }
+        __syncthreads();
+        if (tid < kQcCols) {
+            double O = 0.0, Ls = 0.0;
+            for (int q = 0; q < n_used; ++q) {
+                O = fma(L.u.s4.f[q], L.u.s4.mo[q][tid], O);
+                Ls = fma(L.u.s4.f[q], L.u.s4.ml[q], Ls);
+            }
+            publish_f32(ws->oc_t[h][kQcCols * k + tid], (float)(O / Ls), tag);
+        }
+        // o_c of head h, columns 64 wave .. 64 wave + 63 (two per lane)
+        poll16(ws->oc_t, 8 * (h * kLora + 64 * wave + 2 * lane), lane < 32, tag, v, ws);
+        if (lane < 32) {
+            L.u.s4.oc[64 * wave + 2 * lane] = tagged_f32(v.x, v.y);
+            L.u.s4.oc[64 * wave + 2 * lane + 1] = tagged_f32(v.z, v.w);
+        }
+        __syncthreads();
+        float ov[8];
 #pragma unroll
-    for (int j = 0; j < kPerWave; ++j) {
-        const int i = wave + kWaves * j;
-        const double e = i < n ? exp(s[i] - m) : 0.0;
-        const uint32_t cw[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
+        for (int jj = 0; jj < 8; ++jj) ov[jj] = L.u.s4.oc[64 * wave + 8 * (lane & 7) + jj];
+        const double a = sum8_lanes(dot8_xf(wuv, ov, 0.0));
+        if ((lane & 7) == 0) L.u.s4.uvr[wave][lane >> 3] = a;
+        __syncthreads();
+        if (tid < kUvRows) {
+            double s = 0.0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            o[2 * q] = fma(e, (double)bf_lo(cw[q]), o[2 * q]);
-            o[2 * q + 1] = fma(e, (double)bf_hi(cw[q]), o[2 * q + 1]);
+            for (int w = 0; w < kWaves; ++w) s += L.u.s4.uvr[w][tid];
+            const float ob = bf16r((float)s);
+            st_agent(&ws->out_t[h * kV + kUvRows * k + tid], tag | bf16_bits(ob));
+        }
+        __syncthreads();
+    }
+
+    // ---- S5: o_proj rows 8 wg .. 8 wg + 7 and the residual add
+    {
+        u32x4 v;
+        poll16(ws->out_t, 4 * (256 * wave + 4 * lane), true, tag, v, ws);
+        reinterpret_cast<uint2*>(L.u.s5.outv)[64 * wave + lane] =
+            make_uint2((v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16));
+        __syncthreads();
+        const u32x4* hv = reinterpret_cast<const u32x4*>(L.u.s5.outv + 256 * wave + 32 * (lane & 7));
+        double a = 0.0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a = dot8_x(wo[m], hv[m], a);
+        a = sum8_lanes(a);
+        if ((lane & 7) == 0) L.u.s5.opr[wave][lane >> 3] = a;
+        __syncthreads();
+        if (tid < kOpRows) {
+            double s = 0.0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) s += L.u.s5.opr[w][tid];
+            P.x_out[kOpRows * wg + tid] = bf16r(x_own + bf16r((float)s));
         }
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) part[wave][8 * lane + j] = o[j];
-    __syncthreads();
-    double acc = 0.0;
-#pragma unroll
-    for (int w8 = 0; w8 < kWaves; ++w8) acc += part[w8][tid];
-    ws->part_o[h][k][tid] = acc;
     if (tid == 0) {
-        double l = 0.0;
-        for (int i = 0; i < n; ++i) l += exp(s[i] - m);
-        ws->part_m[h][k] = m;
-        ws->part_l[h][k] = l;
+        const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&ws->epoch, epoch);
     }
 }
 
-// ---------------------------------------------------------------- combine
-// Workgroup (h, g): the head's chunks merged into o_c (512, all threads), then
-// outputs 16 g .. 16 g + 15 of W_UV o_c (a wave per two rows), bf16.
-__global__ __launch_bounds__(kThreads, 1) void combine_kernel(const uint16_t* kv_b, Pos P,
-                                                              Workspace* ws) {
-    __shared__ alignas(16) float oc[kLora];
-    const int h = blockIdx.x, g = blockIdx.y;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
-    const int pos = read_pos(P);
-    if (!pos_ok(P, pos)) return;
-    const int n_chunks = pos / kPosChunk + 1;
-    double M = -INFINITY;
-    for (int k = 0; k < n_chunks; ++k) M = fmax(M, ws->part_m[h][k]);
-    double L = 0.0, o = 0.0;
-    for (int k = 0; k < n_chunks; ++k) {
-        const double f = exp(ws->part_m[h][k] - M);
-        L = fma(f, ws->part_l[h][k], L);
-        o = fma(f, ws->part_o[h][k][tid], o);
-    }
-    oc[tid] = (float)(o / L);                                 // o_c, rounded once
-    __syncthreads();
-    const uint16_t* wuv = kv_b + ((int64_t)h * kKvbRowsPerHead + kNope) * kLora;
+// Rows first, first + stride, ... (< end) of a K = 2048 matrix against the
+// packed bf16 vector xq; each wave keeps its next row in flight while it
+// reduces the current one. f(row, value) receives every wave total.
+template <typename F>
+__device__ __forceinline__ void gemv_rows2048(const uint16_t* W, int first, int stride, int end,
+                                              const u32x4 (&xq)[4], F f) {
+    if (first >= end) return;
+    u32x4 w[4], wn[4];
+    load_row(W, first, w);
+    for (int row = first; row < end; row += stride) {
+        const int nxt = row + stride;
+        if (nxt < end) load_row(W, nxt, wn);
+        f(row, dot_row(w, xq));
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int dv = 16 * g + 2 * wave + r;
-        const u32x4 w8 = reinterpret_cast<const u32x4*>(wuv + (int64_t)dv * kLora)[lane];
-        const float a = (float)wave_sum64(dot8_xf(w8, oc + 8 * lane, 0.0));
-        if (lane == 0) ws->out[h * kV + dv] = (uint16_t)bf16_bits(a);
+        for (int m = 0; m < 4; ++m) w[m] = wn[m];
     }
-}
-
-// ---------------------------------------------------------------- oproj
-// Workgroup w: rows 8 w .. 8 w + 7, one per wave; x_out = bf16(x + bf16(o_proj . out)).
-// Each output element is read from x and written to x_out by the same lane,
-// so x_out may alias x.
-__global__ __launch_bounds__(kThreads, 1) void oproj_kernel(const uint16_t* W, const float* x,
-                                                            float* x_out, const Workspace* ws) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const int n = 8 * blockIdx.x + wave;
-    u32x4 w[4], xq[4];
-    load_row(W, n, w);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(ws->out)[lane + kLanes * m];
-    const float a = dot_row(w, xq);
-    if (lane == 0) x_out[n] = bf16r(x[n] + bf16r(a));
 }
 
 // ---------------------------------------------------------------- embed / lm_head / argmax
@@ -408,7 +694,10 @@ __global__ __launch_bounds__(kThreads, 1) void lmhead_kernel(const float* x, con
     __shared__ float bv_s[kWaves];
     __shared__ int bi_s[kWaves];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    norm2048(x, norm, eps, xb, red);
+    const float4 xv = reinterpret_cast<const float4*>(x)[threadIdx.x];
+    const uint2 gb = norm ? reinterpret_cast<const uint2*>(norm)[threadIdx.x]
+                          : make_uint2(0x3f803f80u, 0x3f803f80u);
+    norm2048(xv, gb, eps, xb, red);
     u32x4 xq[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(xb)[lane + kLanes * m];
@@ -498,27 +787,28 @@ extern "C" int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, 
         return FLEET_MOE_ERR_ARG;
     if (workspace_bytes < sizeof(attn::Workspace)) return FLEET_MOE_ERR_WORKSPACE;
     if (int e = fleet_moe_check_device(attn::kWG)) return e;
-    auto* ws = static_cast<attn::Workspace*>(workspace);
-    const float eps = dims->rms_eps;
-    const attn::Pos P = {pos_dev, pos, max_pos};
-    // with a device position the grid covers every chunk of max_pos (chunks
-    // past the position return at once)
-    const int span = pos_dev ? max_pos : pos + 1;
-    const int n_chunks = (span + attn::kPosChunk - 1) / attn::kPosChunk;
+    attn::Params P;
+    P.x = x;
+    P.x_out = x_out;
+    P.norm_in = layer->norm_in;
+    P.qkv = layer->qkv;
+    P.kv_a_norm = layer->kv_a_norm;
+    P.kv_b = layer->kv_b;
+    P.o_proj = layer->o_proj;
+    P.cache = cache;
+    P.cos = rope_cos;
+    P.sin = rope_sin;
+    P.pos_dev = pos_dev;
+    P.pos_host = pos;
+    P.max_pos = max_pos;
     // (qk_nope + qk_rope)^-0.5 * mscale(40, 0.707)^2 (src/host/reference_decode.py:
     // 78-83, 197-203), in double
     const double m = 0.1 * 0.707 * std::log(40.0) + 1.0;
-    const double scale = std::pow(192.0, -0.5) * m * m;
-    hipLaunchKernelGGL(attn::qkv_kernel, dim3(attn::kWG), dim3(attn::kThreads), 0, stream, x,
-                       layer->norm_in, layer->qkv, eps, ws);
-    hipLaunchKernelGGL(attn::prep_kernel, dim3(attn::kHeads + 1), dim3(attn::kThreads), 0, stream,
-                       layer->kv_b, layer->kv_a_norm, rope_cos, rope_sin, P, cache, eps, ws);
-    hipLaunchKernelGGL(attn::mla_kernel, dim3(attn::kHeads, n_chunks), dim3(attn::kThreads), 0,
-                       stream, cache, P, scale, ws);
-    hipLaunchKernelGGL(attn::combine_kernel, dim3(attn::kHeads, attn::kV / 16),
-                       dim3(attn::kThreads), 0, stream, layer->kv_b, P, ws);
-    hipLaunchKernelGGL(attn::oproj_kernel, dim3(kHidden / 8), dim3(attn::kThreads), 0, stream,
-                       layer->o_proj, x, x_out, ws);
+    P.scale = std::pow(192.0, -0.5) * m * m;
+    P.eps = dims->rms_eps;
+    P.ws = static_cast<attn::Workspace*>(workspace);
+    hipLaunchKernelGGL(attn::attn_layer_kernel, dim3(attn::kWG), dim3(attn::kThreads), 0, stream,
+                       P);
     return (int)hipGetLastError();
 }
 

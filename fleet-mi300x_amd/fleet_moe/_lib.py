@@ -21,6 +21,7 @@ ABORT_UNIT_WAIT = 0x2
 ABORT_GROUP_WAIT = 0x4
 ABORT_POSITION = 0x8
 ABORT_TOKEN = 0x10
+ABORT_ATTN_WAIT = 0x20
 
 
 class FleetMoeDims(ctypes.Structure):

@@ -159,7 +159,7 @@ typedef struct fleet_attn_layer {
 } fleet_attn_layer;
 
 /* Workspace bytes fleet_attn_decode, fleet_embed and fleet_lm_head_argmax
- * need (one workspace serves all three; about 4.3 MB). */
+ * need (one workspace serves all three; about 2.4 MB). */
 size_t fleet_attn_workspace_bytes(const fleet_moe_dims* dims);
 
 /* The attention half of one decoder layer at one position:
@@ -178,7 +178,9 @@ size_t fleet_attn_workspace_bytes(const fleet_moe_dims* dims);
  * pos_dev is not NULL, the device int32 *pos_dev read by the kernels, so one
  * captured graph serves every step; a device position outside [0, max_pos)
  * sets FLEET_MOE_ABORT_POSITION in the workspace status and leaves x_out
- * unspecified. Five launches on `stream`. */
+ * unspecified. One launch of 256 workgroups on `stream`, all resident at once
+ * (their stages hand data to each other through the workspace; a stage that
+ * waits past its bound sets FLEET_MOE_ABORT_ATTN_WAIT). */
 int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, float* x_out,
                       uint16_t* cache, int32_t max_pos, int32_t pos, const int32_t* pos_dev,
                       const float* rope_cos, const float* rope_sin, void* workspace,
@@ -216,6 +218,7 @@ int fleet_moe_workspace_status(const void* workspace, uint32_t* status, hipStrea
 #define FLEET_MOE_ABORT_GROUP_WAIT 0x4u   /* grouped step phase never completed */
 #define FLEET_MOE_ABORT_POSITION 0x8u     /* device position outside [0, max_pos) */
 #define FLEET_MOE_ABORT_TOKEN 0x10u       /* device token outside the vocabulary */
+#define FLEET_MOE_ABORT_ATTN_WAIT 0x20u   /* an attention stage never completed */
 
 /* Diagnostic: reads `bytes` of device memory with the weight-streaming load
  * pattern of the kernels above (16-byte non-temporal loads, 1 KB per wave
