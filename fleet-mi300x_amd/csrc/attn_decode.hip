@@ -52,6 +52,10 @@
 
 #include "moe_common.h"
 
+#ifndef FLEET_ATTN_TRACE
+#define FLEET_ATTN_TRACE 0
+#endif
+
 namespace fleet_moe {
 namespace attn {
 
@@ -74,7 +78,7 @@ constexpr int kQcCols = kLora / kChunks;                 // 32 columns of q_c / 
 constexpr int kUkRows = kNope / kWaves;                  // 16 W_UK rows per wave
 constexpr int kUvRows = kV / kChunks;                    // 8 W_UV rows per workgroup
 constexpr int kOpRows = kHidden / kWG;                   // 8 o_proj rows per workgroup
-constexpr int kBatch = 12;                               // cache rows a wave holds at once
+constexpr int kBatch = 9;                                // cache rows a wave holds at once (72-row chunks: one batch)
 static_assert(kHeads * kChunks == kWG && kQcCols * kChunks == kLora, "work split");
 static_assert(kUvRows == kWaves && kOpRows == kWaves, "one row per wave in the epilogues");
 static_assert(kBatch <= kLanes, "one lane per row for the exponentials");
@@ -169,6 +173,96 @@ __device__ __forceinline__ double wave_max64(double v) {
     return fmax(fmax(readlane64(v, 0), readlane64(v, 16)), fmax(readlane64(v, 32), readlane64(v, 48)));
 }
 
+// The fp64 counterpart of wave_msum (moe_common.h): N values per lane summed
+// over the wave in six exchange steps (lane L with L ^ {1, 2, 7, 15, 16, 32});
+// v[0] of lane L returns the total of value msum_index<N>(L).
+template <int K>
+__device__ __forceinline__ double msum_xchg64(double x) {
+    const long long b = __double_as_longlong(x);
+    int lo = (int)(b & 0xffffffffll), hi = (int)(b >> 32);
+    if constexpr (K == 0) {
+        lo = FLEET_DPP(lo, 0xB1); hi = FLEET_DPP(hi, 0xB1);
+    } else if constexpr (K == 1) {
+        lo = FLEET_DPP(lo, 0x4E); hi = FLEET_DPP(hi, 0x4E);
+    } else if constexpr (K == 2) {
+        lo = FLEET_DPP(lo, 0x141); hi = FLEET_DPP(hi, 0x141);
+    } else if constexpr (K == 3) {
+        lo = FLEET_DPP(lo, 0x140); hi = FLEET_DPP(hi, 0x140);
+    } else if constexpr (K == 4) {
+        lo = __builtin_amdgcn_ds_swizzle(lo, 0x401F); hi = __builtin_amdgcn_ds_swizzle(hi, 0x401F);
+    } else {
+        const int a = (int)(((threadIdx.x & (kLanes - 1)) ^ 32u) << 2);
+        lo = __builtin_amdgcn_ds_bpermute(a, lo); hi = __builtin_amdgcn_ds_bpermute(a, hi);
+    }
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+template <int K, int LEN, int N>
+__device__ __forceinline__ void msum_step64(double (&v)[N]) {
+    if constexpr (K < 6) {
+        if constexpr (LEN > 1) {
+            const bool up = __builtin_popcount((threadIdx.x & (kLanes - 1)) & kMsumDual[K]) & 1;
+#pragma unroll
+            for (int j = 0; j < LEN / 2; ++j) {
+                const double lo = v[j] + msum_xchg64<K>(v[j]);
+                const double hi = v[j + LEN / 2] + msum_xchg64<K>(v[j + LEN / 2]);
+                v[j] = up ? hi : lo;
+            }
+            msum_step64<K + 1, LEN / 2, N>(v);
+        } else {
+            v[0] += msum_xchg64<K>(v[0]);
+            msum_step64<K + 1, 1, N>(v);
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ double wave_msum64(double (&v)[N]) {
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N is a power of two <= 64");
+    msum_step64<0, N, N>(v);
+    return v[0];
+}
+
+// The lowest lane that receives value i of wave_msum<N> / wave_msum64<N>.
+constexpr int msum_index_c(int n, int lane) {
+    int idx = 0;
+    for (int k = 0; (1 << k) < n; ++k) {
+        int m = lane & kMsumDual[k], p = 0;
+        while (m) { p ^= m & 1; m >>= 1; }
+        idx = (idx << 1) | p;
+    }
+    return idx;
+}
+constexpr int msum_lane_of(int n, int i) {
+    for (int lane = 0; lane < kLanes; ++lane)
+        if (msum_index_c(n, lane) == i) return lane;
+    return -1;
+}
+struct LaneTable16 {
+    int lane[16];
+};
+constexpr LaneTable16 make_lane_table16() {
+    LaneTable16 t{};
+    for (int i = 0; i < 16; ++i) t.lane[i] = msum_lane_of(16, i);
+    return t;
+}
+constexpr LaneTable16 kMsumLane16 = make_lane_table16();
+static_assert(kMsumLane16.lane[0] == 0 && kMsumLane16.lane[15] >= 0, "lane table");
+
+// bf16 chunk against 8 fp64 values (fp32 values widened once): each product
+// is exact in fp64 and rounded once into the fp64 sum.
+__device__ __forceinline__ double dot8_xd(const u32x4& w, const double* x, double acc) {
+    acc = fma((double)bf_lo(w.x), x[0], acc);
+    acc = fma((double)bf_hi(w.x), x[1], acc);
+    acc = fma((double)bf_lo(w.y), x[2], acc);
+    acc = fma((double)bf_hi(w.y), x[3], acc);
+    acc = fma((double)bf_lo(w.z), x[4], acc);
+    acc = fma((double)bf_hi(w.z), x[5], acc);
+    acc = fma((double)bf_lo(w.w), x[6], acc);
+    acc = fma((double)bf_hi(w.w), x[7], acc);
+    return acc;
+}
+
 // DeepseekV2 RoPE of 64 bf16-valued inputs v: reordered basis y = [v0, v2, ..,
 // v62, v1, v3, .., v63]; out[i] = y[i] cos[i] - y[i+32] sin[i] (i < 32),
 // y[i] cos[i] + y[i-32] sin[i] (i >= 32), two products and a sum, unfused, as
@@ -204,11 +298,19 @@ __device__ __forceinline__ bool tagged(const u32x4& v, uint32_t tag) {
 __device__ bool poll16(const void* base, int off, bool active, uint32_t tag, u32x4& v,
                        Workspace* ws) {
     const __amdgpu_buffer_rsrc_t r = rsrc(base);
-    for (uint32_t it = 0;; ++it) {
-        v = active ? ld_dev16(r, off) : u32x4{0u, 0u, 0u, 0u};
-        if (__all(!active || tagged(v, tag))) return true;
-        if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&ws->abort) != 0)) {
+    const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+    // two polls in flight, half a round trip apart
+    u32x4 a = active ? ld_dev16(r, off) : z;
+    __builtin_amdgcn_s_sleep(8);
+    u32x4 b = active ? ld_dev16(r, off) : z;
+    for (uint32_t it = 0;; it += 2) {
+        if (__all(!active || tagged(a, tag))) { v = a; return true; }
+        a = active ? ld_dev16(r, off) : z;
+        if (__all(!active || tagged(b, tag))) { v = b; return true; }
+        b = active ? ld_dev16(r, off) : z;
+        if (it >= kSpinLimit || ((it & 1022) == 1022 && ld_agent(&ws->abort) != 0)) {
             if ((threadIdx.x & (kLanes - 1)) == 0) raise(ws, FLEET_MOE_ABORT_ATTN_WAIT);
+            v = a;
             return false;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -258,7 +360,21 @@ struct Params {
     double scale;
     float eps;
     Workspace* ws;
+#if FLEET_ATTN_TRACE
+    unsigned long long* trace;   // [kWG][kWaves][16] s_memrealtime stamps, or null
+#endif
 };
+
+#if FLEET_ATTN_TRACE
+#define ATTN_TRACE(k)                                                                    \
+    do {                                                                                 \
+        if (P.trace && lane == 0)                                                        \
+            P.trace[((size_t)wg * kWaves + wave) * 16 + (k)] =                           \
+                __builtin_amdgcn_s_memrealtime();                                        \
+    } while (0)
+#else
+#define ATTN_TRACE(k) do {} while (0)
+#endif
 
 struct Lds {
     alignas(16) uint32_t xb[kHidden / 2];      // x_norm as bf16 pairs
@@ -299,6 +415,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         if (wg == 0 && tid == 0) raise(ws, FLEET_MOE_ABORT_POSITION);
         return;
     }
+    ATTN_TRACE(0);
     const int h = (wg >> 3) & (kHeads - 1);
     const int k = (wg & 7) + 8 * (wg >> 7);
     const int n_pos = pos + 1;
@@ -309,7 +426,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     const bool has_rows = k < n_used;
     const bool last = k == n_used - 1;                  // the chunk holding `pos`
 
-    // ---- everything this workgroup will read, in order of need
+    // ---- the inputs of the first stage
     const uint32_t epoch = ld_agent(&ws->epoch) + 1u;
     const uint32_t tag = (epoch & 0xffffu) << 16;
     const float4 xv = reinterpret_cast<const float4*>(P.x)[tid];
@@ -321,6 +438,31 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     u32x4 wq0[4], wq1[4];
     load_row(P.qkv, r0, wq0);
     if (r1 < kQkvRows) load_row(P.qkv, r1, wq1);
+    ATTN_TRACE(1);
+    // ---- S1: RMSNorm, then this wave's rows of [q_proj ; kv_a]
+    norm2048(xv, gb, P.eps, L.xb, L.red);
+    ATTN_TRACE(2);
+    {
+        u32x4 xq[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
+        const float a0 = bf16r(dot_row(wq0, xq));
+        if (lane == 0) {
+            ws->qkv[r0] = a0;
+            st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
+        }
+        if (r1 < kQkvRows) {
+            const float a1 = bf16r(dot_row(wq1, xq));
+            if (lane == 0) {
+                ws->qkv[r1] = a1;
+                st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
+            }
+        }
+    }
+
+    // The other stages' weight slices and cache rows go in flight now, behind
+    // the first stage's inputs: issued before the RMSNorm, these ~30 loads
+    // per wave would hold up x and the q / kv_a rows.
     // W_UK of head h: row 16 wave + lane / 4, columns 32 k + 8 (lane % 4) .. + 7
     const u32x4 wuk = ld_stream(reinterpret_cast<const u32x4*>(
         P.kv_b + ((int64_t)h * kKvbRowsPerHead + kUkRows * wave + (lane >> 2)) * kLora +
@@ -356,31 +498,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         for (int m = 0; m < 4; ++m) wo[m] = ld_stream(p + m);
     }
 
-    // ---- S1: RMSNorm, then this wave's rows of [q_proj ; kv_a]
-    norm2048(xv, gb, P.eps, L.xb, L.red);
-    {
-        u32x4 xq[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
-        const float a0 = bf16r(dot_row(wq0, xq));
-        if (lane == 0) {
-            ws->qkv[r0] = a0;
-            st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
-        }
-        if (r1 < kQkvRows) {
-            const float a1 = bf16r(dot_row(wq1, xq));
-            if (lane == 0) {
-                ws->qkv[r1] = a1;
-                st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
-            }
-        }
-    }
-
+    ATTN_TRACE(3);
     // ---- S2: q_c[h][32k .. 32k+31] = sum over the 128 rows of W_UK q_nope
     {
         u32x4 qn;
         poll16(ws->qkv_t, 4 * (h * (kNope + kRope) + kUkRows * wave) + 16 * lane, lane < 4,
                tag, qn, ws);
+        ATTN_TRACE(4);
         // lane needs q_nope[16 wave + lane / 4]: word (lane / 4) % 4 of lane lane / 16
         const int src = (lane >> 4) << 2;
         const uint32_t c0 = __builtin_amdgcn_ds_bpermute(src, qn.x);
@@ -417,6 +541,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         }
         __syncthreads();
     }
+    ATTN_TRACE(5);
 
     // ---- S3: the chunk's scores and fp64 softmax partial
     const float* cs = P.cos + (int64_t)pos * kRope;
@@ -450,6 +575,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
                 L.u.s3.kva[w0 + 4 * lane + 3] = __uint_as_float(v.w << 16);
             }
         }
+        ATTN_TRACE(6);
         __syncthreads();
         if (tid < kRope) {
             const float qp = rope_one(L.u.s3.qpe_raw, cs, sn, tid);
@@ -483,68 +609,77 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         }
         __syncthreads();
 
-        float qcl[8];
+        double qd[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) qcl[jj] = L.u.s3.qc[8 * lane + jj];
+        for (int jj = 0; jj < 8; ++jj) qd[jj] = (double)L.u.s3.qc[8 * lane + jj];
         const float qp = L.u.s3.qpe[lane];
-        const u32x4 rc = reinterpret_cast<const u32x4*>(L.u.s3.row)[lane];
-        const float rk = __uint_as_float((uint32_t)L.u.s3.row[kLora + lane] << 16);
+        constexpr int kSum = 16;                           // kBatch rows reduced together
+        static_assert(kBatch <= kSum, "one reduction per batch");
+        int ri = 0;                                        // the row whose score this lane gets
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2)
+            ri = (ri << 1) | (__builtin_popcount(lane & kMsumDual[k2]) & 1);
         double m_w = -INFINITY, l_w = 0.0;
         double o[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
-        for (int base = t0 + wave, b = 0; base < t1; base += kWaves * kBatch, ++b) {
+        // rows before `pos`, kBatch at a time (rows past the chunk are zeros);
+        // online softmax: rescale by exp(m_old - m_new), add exp(s - m_new) c
+        for (int base = t0 + wave, b = 0; base < t_end; base += kWaves * kBatch, ++b) {
             if (b > 0) {
 #pragma unroll
                 for (int i = 0; i < kBatch; ++i) {
-                    const int t = base + kWaves * i;
-                    if (t < t_end) {
-                        const uint16_t* row = P.cache + (int64_t)t * kRowElems;
-                        c8[i] = reinterpret_cast<const u32x4*>(row)[lane];
-                        kp[i] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
-                    }
+                    const int t = min(base + kWaves * i, t_end - 1);   // clamped: a real row
+                    const uint16_t* row = P.cache + (int64_t)t * kRowElems;
+                    c8[i] = reinterpret_cast<const u32x4*>(row)[lane];
+                    kp[i] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
                 }
             }
-            double s[kBatch];
-            double mb = -INFINITY;
+            double a[kSum];
 #pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-                const int t = base + kWaves * i;
-                s[i] = -INFINITY;
-                if (t < t1) {
-                    const bool cur = t == pos;
-                    const u32x4 cv = cur ? rc : c8[i];
-                    const float kv = cur ? rk : kp[i];
-                    double a = dot8_xf(cv, qcl, 0.0);
-                    a += (double)(kv * qp);                    // bf16 x bf16: exact
-                    s[i] = wave_sum64(a) * P.scale;
-                    mb = fmax(mb, s[i]);
-                }
-            }
-            const double m_new = fmax(m_w, mb);
+            for (int i = 0; i < kSum; ++i)
+                a[i] = i < kBatch ? dot8_xd(c8[i], qd, (double)(kp[i] * qp)) : 0.0;
+            const double tot = wave_msum64(a);
+            const bool valid = ri < kBatch && base + kWaves * ri < t_end;
+            const double sv = valid ? tot * P.scale : -INFINITY;
+            const double m_new = fmax(m_w, wave_max64(sv));
             const double fo = exp(m_w - m_new);            // 0 while nothing is accumulated
-            double sv = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < kBatch; ++i) sv = lane == i ? s[i] : sv;
-            const double ev = exp(sv - m_new);             // one row per lane; exp(-inf) = 0
+            const double ev = exp(sv - m_new);             // 0 for rows that are not there
             l_w *= fo;
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) o[jj] *= fo;
 #pragma unroll
             for (int i = 0; i < kBatch; ++i) {
-                const int t = base + kWaves * i;
-                if (t < t1) {
-                    const double e = readlane64(ev, i);
-                    const u32x4 cv = t == pos ? rc : c8[i];
-                    const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
-                    l_w += e;
+                const double e = readlane64(ev, kMsumLane16.lane[i]);
+                uint32_t cw[4] = {c8[i].x, c8[i].y, c8[i].z, c8[i].w};
+                // widen again rather than keep the score loop's 96 widened values
+                // alive across the reduction (the compiler would share them)
+                asm("" : "+v"(cw[0]), "+v"(cw[1]), "+v"(cw[2]), "+v"(cw[3]));
+                l_w += e;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        o[2 * q] = fma(e, (double)bf_lo(cw[q]), o[2 * q]);
-                        o[2 * q + 1] = fma(e, (double)bf_hi(cw[q]), o[2 * q + 1]);
-                    }
+                for (int q = 0; q < 4; ++q) {
+                    o[2 * q] = fma(e, (double)bf_lo(cw[q]), o[2 * q]);
+                    o[2 * q + 1] = fma(e, (double)bf_hi(cw[q]), o[2 * q + 1]);
                 }
             }
             m_w = m_new;
         }
+        // the row of `pos`, derived from kv_a above
+        if (last && (pos - t0) % kWaves == wave) {
+            const u32x4 rc = reinterpret_cast<const u32x4*>(L.u.s3.row)[lane];
+            const float rk = __uint_as_float((uint32_t)L.u.s3.row[kLora + lane] << 16);
+            const double sv = wave_sum64(dot8_xd(rc, qd, (double)(rk * qp))) * P.scale;
+            const double m_new = fmax(m_w, sv);
+            const double fo = exp(m_w - m_new);
+            const double e = exp(sv - m_new);
+            const uint32_t cw[4] = {rc.x, rc.y, rc.z, rc.w};
+            l_w = fma(l_w, fo, e);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                o[2 * q] = fma(e, (double)bf_lo(cw[q]), o[2 * q] * fo);
+                o[2 * q + 1] = fma(e, (double)bf_hi(cw[q]), o[2 * q + 1] * fo);
+            }
+            m_w = m_new;
+        }
+        ATTN_TRACE(8);
         if (lane == 0) {
             L.u.s3.wm[wave] = m_w;
             L.u.s3.wl[wave] = l_w;
@@ -569,6 +704,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             publish_f64(&ws->ml_t[h][k][4], Ls, tag);
         }
     }
+    ATTN_TRACE(9);
     __syncthreads();
 
     // ---- S4: o_c[h][32k .. 32k+31] from the chunk partials, then W_UV rows 8k .. 8k+7
@@ -586,6 +722,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             if (lane & 1) L.u.s4.ml[cm] = tagged_f64(v);
             else L.u.s4.mm[cm] = tagged_f64(v);
         }
+        ATTN_TRACE(10);
         __syncthreads();
         if (tid < kChunks) {
             double M = -INFINITY;
@@ -601,8 +738,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             }
             publish_f32(ws->oc_t[h][kQcCols * k + tid], (float)(O / Ls), tag);
         }
+        ATTN_TRACE(11);
         // o_c of head h, columns 64 wave .. 64 wave + 63 (two per lane)
         poll16(ws->oc_t, 8 * (h * kLora + 64 * wave + 2 * lane), lane < 32, tag, v, ws);
+        ATTN_TRACE(12);
         if (lane < 32) {
             L.u.s4.oc[64 * wave + 2 * lane] = tagged_f32(v.x, v.y);
             L.u.s4.oc[64 * wave + 2 * lane + 1] = tagged_f32(v.z, v.w);
@@ -623,11 +762,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         }
         __syncthreads();
     }
+    ATTN_TRACE(13);
 
     // ---- S5: o_proj rows 8 wg .. 8 wg + 7 and the residual add
     {
         u32x4 v;
         poll16(ws->out_t, 4 * (256 * wave + 4 * lane), true, tag, v, ws);
+        ATTN_TRACE(14);
         reinterpret_cast<uint2*>(L.u.s5.outv)[64 * wave + lane] =
             make_uint2((v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16));
         __syncthreads();
@@ -645,6 +786,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             P.x_out[kOpRows * wg + tid] = bf16r(x_own + bf16r((float)s));
         }
     }
+    ATTN_TRACE(15);
     if (tid == 0) {
         const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
@@ -762,6 +904,11 @@ int fleet_moe_check_device(int min_cus);
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+#if FLEET_ATTN_TRACE
+static unsigned long long* g_attn_trace = nullptr;
+extern "C" void fleet_attn_debug_set_trace(void* p) { g_attn_trace = (unsigned long long*)p; }
+#endif
+
 extern "C" size_t fleet_attn_workspace_bytes(const fleet_moe_dims* dims) {
     if (fleet_moe_check_dims(dims) != 0) return 0;
     return (sizeof(attn::Workspace) + 255) & ~(size_t)255;
@@ -807,6 +954,9 @@ extern "C" int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, 
     P.scale = std::pow(192.0, -0.5) * m * m;
     P.eps = dims->rms_eps;
     P.ws = static_cast<attn::Workspace*>(workspace);
+#if FLEET_ATTN_TRACE
+    P.trace = g_attn_trace;
+#endif
     hipLaunchKernelGGL(attn::attn_layer_kernel, dim3(attn::kWG), dim3(attn::kThreads), 0, stream,
                        P);
     return (int)hipGetLastError();
