@@ -118,8 +118,9 @@ __device__ __forceinline__ void raise(Workspace* ws, uint32_t bit) {
 
 // RMSNorm of a 2048-vector held 4 per thread (512 threads), the arithmetic of
 // the MoE decode kernel (fp64 sum of squares, correctly rounded sqrt and
-// division, two bf16 roundings); writes the bf16 result as packed pairs.
-__device__ void norm2048(const float4 xv, const uint2 gb, float eps, uint32_t* xb, double* red) {
+// division, two bf16 roundings); writes the bf16 result as packed pairs and
+// returns its 2-norm (for the certified GEMVs). red: 16 doubles of LDS.
+__device__ float norm2048(const float4 xv, const uint2 gb, float eps, uint32_t* xb, double* red) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
     double ss = (double)xv.x * xv.x + (double)xv.y * xv.y + (double)xv.z * xv.z +
                 (double)xv.w * xv.w;
@@ -138,7 +139,14 @@ __device__ void norm2048(const float4 xv, const uint2 gb, float eps, uint32_t* x
     y[3] = bf16r(y[3] * bf_hi(gb.y));
     xb[2 * tid] = bf16_bits(y[0]) | (bf16_bits(y[1]) << 16);
     xb[2 * tid + 1] = bf16_bits(y[2]) | (bf16_bits(y[3]) << 16);
+    const double q = wave_sum64((double)y[0] * y[0] + (double)y[1] * y[1] +
+                                (double)y[2] * y[2] + (double)y[3] * y[3]);
+    if (lane == 0) red[kWaves + wave] = q;
     __syncthreads();
+    double qs = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) qs += red[kWaves + w];
+    return (float)__builtin_sqrt(qs);
 }
 
 __device__ __forceinline__ void load_row(const uint16_t* W, int64_t row, u32x4 (&w)[4]) {
@@ -154,6 +162,24 @@ __device__ __forceinline__ float dot_row(const u32x4 (&w)[4], const u32x4 (&xq)[
 #pragma unroll
     for (int m = 0; m < 4; ++m) a = dot8_x(w[m], xq[m], a);
     return (float)wave_sum64(a);
+}
+
+// bf16 of the exactly rounded dot of a K = 2048 bf16 row with a bf16 vector
+// of 2-norm xnorm: the fp32 evaluation (v_dot2 chains of depth 8, a two-level
+// tree, the wave sum: 16 roundings) when certify_bf16 proves its bf16
+// rounding, dot_row otherwise.
+__device__ __forceinline__ float dot_row_bf16(const u32x4 (&w)[4], const u32x4 (&xq)[4],
+                                              float xnorm) {
+    float a[4], n[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        a[m] = dot8_d2(w[m], xq[m], 0.f);
+        n[m] = dot8_d2(w[m], w[m], 0.f);
+    }
+    float r;
+    if (!certify_bf16(wave_sum(tree_sum(a)), wave_sum(tree_sum(n)), xnorm, cert_gamma(16), r))
+        r = bf16r(dot_row(w, xq));
+    return r;
 }
 
 // Sum over the 8 lanes of each aligned group of 8 (quad exchanges, then the
@@ -378,7 +404,7 @@ struct Params {
 
 struct Lds {
     alignas(16) uint32_t xb[kHidden / 2];      // x_norm as bf16 pairs
-    double red[kWaves];
+    double red[2 * kWaves];
     union {
         struct {                                // S2
             double uk[kWaves][kUkRows][kQcCols];
@@ -440,19 +466,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     if (r1 < kQkvRows) load_row(P.qkv, r1, wq1);
     ATTN_TRACE(1);
     // ---- S1: RMSNorm, then this wave's rows of [q_proj ; kv_a]
-    norm2048(xv, gb, P.eps, L.xb, L.red);
+    const float xnorm = norm2048(xv, gb, P.eps, L.xb, L.red);
     ATTN_TRACE(2);
     {
         u32x4 xq[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
-        const float a0 = bf16r(dot_row(wq0, xq));
+        const float a0 = dot_row_bf16(wq0, xq, xnorm);
         if (lane == 0) {
             ws->qkv[r0] = a0;
             st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
         }
         if (r1 < kQkvRows) {
-            const float a1 = bf16r(dot_row(wq1, xq));
+            const float a1 = dot_row_bf16(wq1, xq, xnorm);
             if (lane == 0) {
                 ws->qkv[r1] = a1;
                 st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
@@ -795,18 +821,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
 }
 
 // Rows first, first + stride, ... (< end) of a K = 2048 matrix against the
-// packed bf16 vector xq; each wave keeps its next row in flight while it
-// reduces the current one. f(row, value) receives every wave total.
+// packed bf16 vector xq (2-norm xnorm); each wave keeps its next row in
+// flight while it reduces the current one. f(row, value) receives every
+// row's exactly rounded bf16 result.
 template <typename F>
 __device__ __forceinline__ void gemv_rows2048(const uint16_t* W, int first, int stride, int end,
-                                              const u32x4 (&xq)[4], F f) {
+                                              const u32x4 (&xq)[4], float xnorm, F f) {
     if (first >= end) return;
     u32x4 w[4], wn[4];
     load_row(W, first, w);
     for (int row = first; row < end; row += stride) {
         const int nxt = row + stride;
         if (nxt < end) load_row(W, nxt, wn);
-        f(row, dot_row(w, xq));
+        f(row, dot_row_bf16(w, xq, xnorm));
 #pragma unroll
         for (int m = 0; m < 4; ++m) w[m] = wn[m];
     }
@@ -832,21 +859,21 @@ __global__ __launch_bounds__(kThreads, 1) void lmhead_kernel(const float* x, con
                                                              const uint16_t* W, float eps,
                                                              float* logits, Workspace* ws) {
     __shared__ alignas(16) uint32_t xb[kHidden / 2];
-    __shared__ double red[kWaves];
+    __shared__ double red[2 * kWaves];
     __shared__ float bv_s[kWaves];
     __shared__ int bi_s[kWaves];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
     const float4 xv = reinterpret_cast<const float4*>(x)[threadIdx.x];
     const uint2 gb = norm ? reinterpret_cast<const uint2*>(norm)[threadIdx.x]
                           : make_uint2(0x3f803f80u, 0x3f803f80u);
-    norm2048(xv, gb, eps, xb, red);
+    const float xnorm = norm2048(xv, gb, eps, xb, red);
     u32x4 xq[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(xb)[lane + kLanes * m];
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    gemv_rows2048(W, blockIdx.x + kWG * wave, kWG * kWaves, kVocab, xq, [&](int row, float a) {
-        const float v = bf16r(a);
+    gemv_rows2048(W, blockIdx.x + kWG * wave, kWG * kWaves, kVocab, xq, xnorm,
+                  [&](int row, float v) {
         if (logits && lane == 0) logits[row] = v;
         if (v > bv || (v == bv && row < bi)) {
             bv = v;

@@ -4,8 +4,10 @@
 //   * bf16 rounding is round-to-nearest-even on the fp32 bit pattern;
 //   * reductions whose result must be reproducible bit for bit (RMSNorm mean of
 //     squares, router logits, softmax) run in fp64 and are rounded once to fp32;
-//   * expert GEMVs accumulate in fp32 and reduce in one fixed order (DPP
-//     row reductions, then the four rows in lane order).
+//   * every bf16 GEMV result is the exact dot product rounded once to fp32
+//     and then to bf16: an fp32 evaluation is accepted when a rigorous error
+//     bound proves its bf16 rounding equal to the exact one (certify_bf16),
+//     and the exact fp64 sum of the exact products is used otherwise.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -110,6 +112,55 @@ __device__ __forceinline__ double dot8_xf(const u32x4& w, const float* x, double
     acc = fma((double)bf_hi(w.w), (double)x[7], acc);
     return acc;
 }
+
+// Certified fast path for exactly rounded bf16 results. A dot product of
+// bf16 operands evaluated in fp32 (v_dot2 chains, a fixed summation tree)
+// differs from the exact value s by at most
+//   E = gamma_d * sum |w_i x_i| <= gamma_d * ||w||_2 * ||x||_2,
+// gamma_d = d u / (1 - d u), d the largest number of roundings on any path
+// from a product to the result, u = 2^-23 (one ulp per rounding, whatever
+// rounding v_dot2 uses internally, two roundings per v_dot2). With lo / hi
+// the computed value minus / plus E widened by two of its ulps (so the
+// fp32 subtraction and addition cannot round inwards), every s in [lo, hi]
+// has fp32(s) in [lo, hi]; bf16 rounding is monotone, so when lo and hi
+// round to the same bf16, that value is bf16(fp32(s)) -- the exactly rounded
+// result -- and `out` receives it. Otherwise (a result near a bf16 rounding
+// boundary, non-finite values) the caller evaluates the exact dot product.
+// w2 is the computed sum of w_i^2 and xnorm the computed ||x||_2; the factor
+// 1 + 2^-10 covers their own rounding, the square root's and the bound's,
+// and 2^-100 (1 + ||w|| + xnorm) any flush of values below 2^-126.
+__device__ __forceinline__ float cert_gamma(int depth) {
+    const float du = (float)depth * 1.1920929e-7f;            // d * 2^-23
+    return du / (1.0f - du) * 1.0009766f;                     // * (1 + 2^-10)
+}
+__device__ __forceinline__ bool certify_bf16(float a, float w2, float xnorm, float gamma,
+                                             float& out) {
+    const float wn = __builtin_sqrtf(fmaxf(w2, 0.f));
+    const float e = gamma * wn * xnorm + fabsf(a) * 2.3841858e-7f +
+                    7.8886091e-31f * (1.0f + wn + xnorm);
+    const float lo = a - e, hi = a + e;
+    const uint32_t bl = bf16_bits(lo), bh = bf16_bits(hi);
+    if (bl == bh && __builtin_isfinite(lo) && __builtin_isfinite(hi)) {
+        out = __uint_as_float(bl << 16);
+        return true;
+    }
+    return false;
+}
+
+// Pairwise sum of N values in a fixed tree of depth ceil(log2 N).
+template <int N>
+__device__ __forceinline__ float tree_sum(const float (&v)[N]) {
+    if constexpr (N == 1) {
+        return v[0];
+    } else {
+        constexpr int H = (N + 1) / 2;
+        float a[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) a[i] = (2 * i + 1 < N) ? v[2 * i] + v[2 * i + 1] : v[2 * i];
+        return tree_sum<H>(a);
+    }
+}
+constexpr int tree_depth(int n) { return n <= 1 ? 0 : 1 + tree_depth((n + 1) / 2); }
 
 // Same, both operands bf16 chunks.
 __device__ __forceinline__ float dot8_bb(const u32x4& w, const u32x4& h, float acc) {

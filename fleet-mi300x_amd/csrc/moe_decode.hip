@@ -28,7 +28,9 @@
 //     11 of them shared and routing-independent). Seven streaming waves pull
 //     pairs from an LDS ticket; a pair is 8 x 16-byte non-temporal loads per
 //     lane against x_norm (bf16 pairs in registers);
-//     h = bf16(bf16(silu(bf16(g))) * bf16(u)).
+//     h = bf16(bf16(silu(bf16(g))) * bf16(u)), every dot exactly rounded
+//     (an fp32 evaluation certified by an error bound, fp64 when the bound
+//     cannot decide).
 //   phase D (down + combine): workgroup w owns output rows [8w, 8w+8). Waves
 //     0..5 take routed slot 0..5 for the 8 rows (8 x 2,816 B), waves 6..7 the
 //     shared expert's rows (4 x 5,632 B each): 22.5 KB per wave, issued
@@ -314,21 +316,40 @@ __device__ __forceinline__ void issue_pair(const u32x4* base, int lane, u32x4 (&
     }
 }
 
-// Reduce one gate/up pair and publish its tagged h word.
+// Exact dot of a K = 2048 row (4 chunks per lane) with x: the fp64 sum of the
+// exact products, rounded once to fp32.
+__device__ __forceinline__ float exact_row2048(const u32x4* w, const u32x4 (&xq)[4]) {
+    double a = 0.0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a = dot8_x(w[m], xq[m], a);
+    return (float)wave_sum64(a);
+}
+// Reduce one gate/up pair and publish its tagged h word. bf16(g) and bf16(u)
+// are the exactly rounded values: the fp32 evaluation (four v_dot2 chains of
+// depth 8, a two-level tree, the wave sum: 16 roundings) is certified against
+// ||w|| ||x_norm||, and a row near a bf16 boundary is evaluated exactly.
 __device__ __forceinline__ void finish_pair(const Params& P, int unit, int pair,
                                             const u32x4 (&b)[8], const u32x4 (&xq)[4],
-                                            uint32_t tag) {
+                                            uint32_t tag, float xnorm) {
     const int lane = threadIdx.x & (kLanes - 1);
-    double g = 0.0, u = 0.0;
+    float g[4], u[4], gw[4], uw[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        g = dot8_x(b[m], xq[m], g);
-        u = dot8_x(b[4 + m], xq[m], u);
+        g[m] = dot8_d2(b[m], xq[m], 0.f);
+        u[m] = dot8_d2(b[4 + m], xq[m], 0.f);
+        gw[m] = dot8_d2(b[m], b[m], 0.f);
+        uw[m] = dot8_d2(b[4 + m], b[4 + m], 0.f);
     }
-    const float gs = (float)wave_sum64(g);
-    const float us = (float)wave_sum64(u);
+    const float gs = wave_sum((g[0] + g[1]) + (g[2] + g[3]));
+    const float us = wave_sum((u[0] + u[1]) + (u[2] + u[3]));
+    const float gws = wave_sum((gw[0] + gw[1]) + (gw[2] + gw[3]));
+    const float uws = wave_sum((uw[0] + uw[1]) + (uw[2] + uw[3]));
+    const float gam = cert_gamma(16);
+    float gb, ub;
+    if (!certify_bf16(gs, gws, xnorm, gam, gb)) gb = bf16r(exact_row2048(b, xq));
+    if (!certify_bf16(us, uws, xnorm, gam, ub)) ub = bf16r(exact_row2048(b + 4, xq));
     if (lane == 0) {
-        const float h = bf16r(bf16r(silu_rn(bf16r(gs))) * bf16r(us));
+        const float h = bf16r(bf16r(silu_rn(gb)) * ub);
         st_agent(&P.ws->h[h_offset(unit) + pair], tag | bf16_bits(h));
     }
 }
@@ -460,6 +481,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
 #pragma unroll
     for (int m = 0; m < 4; ++m)
         xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
+    float xnorm;                              // ||x_norm||_2, for the certified GEMVs
+    {
+        double xs = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) xs += L.xsq[w];
+        xnorm = (float)__builtin_sqrt(xs);
+    }
     FLEET_TRACE(1);
 
     // a2 (local): eight router rows per wave, dot2 with fp32 accumulation,
@@ -519,7 +547,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     auto finish = [&](int item, const u32x4 (&b)[8]) {
         int u, p;
         item_of(wg, item, u, p);
-        finish_pair(P, u, p, b, xq, tag);
+        finish_pair(P, u, p, b, xq, tag, xnorm);
     };
     bool exact_sel = false;
     cur = ctl ? -1 : wave;
@@ -588,13 +616,25 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         u32x4 H[3];
         wait_h<3>(P, unit, kInterChunks, tag, H);
         FLEET_TRACE(5);
+        const float hn = __builtin_sqrtf(wave_sum((dot8_d2(H[0], H[0], 0.f) +
+                                                   dot8_d2(H[1], H[1], 0.f)) +
+                                                  dot8_d2(H[2], H[2], 0.f))) * 1.0001f;
+        const float gam = cert_gamma(16);     // v_dot2 chain 8, tree 2, wave sum 6
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            double acc = 0.0;
+            const u32x4* w = &W[3 * r];
+            const float a = wave_sum((dot8_d2(w[0], H[0], 0.f) + dot8_d2(w[1], H[1], 0.f)) +
+                                     dot8_d2(w[2], H[2], 0.f));
+            const float n = wave_sum((dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) +
+                                     dot8_d2(w[2], w[2], 0.f));
+            float d;
+            if (!certify_bf16(a, n, hn, gam, d)) {
+                double acc = 0.0;
 #pragma unroll
-            for (int m = 0; m < 3; ++m) acc = dot8_x(W[3 * r + m], H[m], acc);
-            const float d = (float)wave_sum64(acc);
-            if (lane == 0) L.part[unit][r] = bf16r(d);
+                for (int m = 0; m < 3; ++m) acc = dot8_x(w[m], H[m], acc);
+                d = bf16r((float)wave_sum64(acc));
+            }
+            if (lane == 0) L.part[unit][r] = d;
         }
     } else {
         if (ctl) {
@@ -620,17 +660,38 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         wait_h<6>(P, unit, kSharedChunks, tag, H);
         FLEET_TRACE(5);
         const int rs = 4 * (wave - kTopK);
+        float hq[6];
+#pragma unroll
+        for (int m = 0; m < 6; ++m) hq[m] = dot8_d2(H[m], H[m], 0.f);
+        const float hn =
+            __builtin_sqrtf(wave_sum(((hq[0] + hq[1]) + (hq[2] + hq[3])) + (hq[4] + hq[5]))) *
+            1.0001f;
+        const float gam = cert_gamma(17);     // v_dot2 chain 8, tree 3, wave sum 6
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const u32x4* wr = reinterpret_cast<const u32x4*>(L.sdown + (rs + r) * kSharedRowBytes);
-            double acc = 0.0;
+            u32x4 w[6];
 #pragma unroll
             for (int m = 0; m < 6; ++m) {
                 const int c = lane + kLanes * m;
-                if (c < kSharedChunks) acc = dot8_x(wr[c], H[m], acc);
+                w[m] = c < kSharedChunks ? wr[c] : u32x4{0u, 0u, 0u, 0u};
             }
-            const float d = (float)wave_sum64(acc);
-            if (lane == 0) L.part[0][rs + r] = bf16r(d);
+            float av[6], nv[6];
+#pragma unroll
+            for (int m = 0; m < 6; ++m) {
+                av[m] = dot8_d2(w[m], H[m], 0.f);
+                nv[m] = dot8_d2(w[m], w[m], 0.f);
+            }
+            const float a = wave_sum(((av[0] + av[1]) + (av[2] + av[3])) + (av[4] + av[5]));
+            const float n = wave_sum(((nv[0] + nv[1]) + (nv[2] + nv[3])) + (nv[4] + nv[5]));
+            float d;
+            if (!certify_bf16(a, n, hn, gam, d)) {
+                double acc = 0.0;
+#pragma unroll
+                for (int m = 0; m < 6; ++m) acc = dot8_x(w[m], H[m], acc);
+                d = bf16r((float)wave_sum64(acc));
+            }
+            if (lane == 0) L.part[0][rs + r] = d;
         }
     }
     FLEET_TRACE(6);

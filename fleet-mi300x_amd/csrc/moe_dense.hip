@@ -61,6 +61,7 @@ struct Params {
 struct Lds {
     alignas(16) uint32_t xb[kHidden / 2];
     double red[kWaves];
+    double xsq[kWaves];
     alignas(16) uint32_t hb[kDenseInter / 2];   // h as bf16 pairs
     int next;
 };
@@ -112,10 +113,23 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     y[3] = bf16r(y[3] * bf_hi(gb.y));
     L.xb[2 * tid] = bf16_bits(y[0]) | (bf16_bits(y[1]) << 16);
     L.xb[2 * tid + 1] = bf16_bits(y[2]) | (bf16_bits(y[3]) << 16);
+    {
+        const double q = (double)y[0] * y[0] + (double)y[1] * y[1] + (double)y[2] * y[2] +
+                         (double)y[3] * y[3];
+        const double qs = wave_sum64(q);
+        if (lane == 0) L.xsq[wave] = qs;
+    }
     __syncthreads();
     u32x4 xq[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
+    float xnorm;                              // ||x_norm||_2, for the certified GEMVs
+    {
+        double xs = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) xs += L.xsq[w];
+        xnorm = (float)__builtin_sqrt(xs);
+    }
 
     // Phase G
     auto claim = [&]() -> int {
@@ -127,16 +141,32 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     };
     while (cur >= 0) {
         const int nxt = claim();
-        double g = 0.0, u = 0.0;
+        // bf16(g), bf16(u) exactly rounded: certified fp32 evaluation (depth
+        // 8 + 2 + 6), the exact fp64 sum for a row the bound cannot decide
+        float g[4], u[4], gw[4], uw[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            g = dot8_x(buf[m], xq[m], g);
-            u = dot8_x(buf[4 + m], xq[m], u);
+            g[m] = dot8_d2(buf[m], xq[m], 0.f);
+            u[m] = dot8_d2(buf[4 + m], xq[m], 0.f);
+            gw[m] = dot8_d2(buf[m], buf[m], 0.f);
+            uw[m] = dot8_d2(buf[4 + m], buf[4 + m], 0.f);
         }
-        const float gs = (float)wave_sum64(g);
-        const float us = (float)wave_sum64(u);
+        const float gam = cert_gamma(16);
+        float gb, ub;
+        if (!certify_bf16(wave_sum(tree_sum(g)), wave_sum(tree_sum(gw)), xnorm, gam, gb)) {
+            double a = 0.0;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) a = dot8_x(buf[m], xq[m], a);
+            gb = bf16r((float)wave_sum64(a));
+        }
+        if (!certify_bf16(wave_sum(tree_sum(u)), wave_sum(tree_sum(uw)), xnorm, gam, ub)) {
+            double a = 0.0;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) a = dot8_x(buf[4 + m], xq[m], a);
+            ub = bf16r((float)wave_sum64(a));
+        }
         if (lane == 0) {
-            const float h = bf16r(bf16r(silu_rn(bf16r(gs))) * bf16r(us));
+            const float h = bf16r(bf16r(silu_rn(gb)) * ub);
             st_agent(&ws->h[wg + kWG * cur], tag | bf16_bits(h));
         }
         if (nxt >= 0) issue_pair(gu + (int64_t)(wg + kWG * nxt) * 2 * kRowChunks, lane, buf);
@@ -176,15 +206,28 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
         __hip_atomic_fetch_or(&ws->abort, FLEET_MOE_ABORT_UNIT_WAIT, __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    double acc = 0.0;
+    // bf16(down . h) exactly rounded: certified fp32 evaluation (v_dot2
+    // chain 8, a 22-value tree 5, wave sum 6), exact fp64 sum as fallback
+    u32x4 hv[kDnIters];
+    float av[kDnIters], wv[kDnIters], hq[kDnIters];
 #pragma unroll
     for (int i = 0; i < kDnIters; ++i) {
         const int c = lane + kLanes * i;
-        if (c < kDnChunks) acc = dot8_x(W[i], reinterpret_cast<const u32x4*>(L.hb)[c], acc);
+        hv[i] = c < kDnChunks ? reinterpret_cast<const u32x4*>(L.hb)[c] : u32x4{0u, 0u, 0u, 0u};
+        av[i] = dot8_d2(W[i], hv[i], 0.f);
+        wv[i] = dot8_d2(W[i], W[i], 0.f);
+        hq[i] = dot8_d2(hv[i], hv[i], 0.f);
     }
-    const float d = (float)wave_sum64(acc);
+    const float hn = __builtin_sqrtf(wave_sum(tree_sum(hq))) * 1.0001f;
+    float out;
+    if (!certify_bf16(wave_sum(tree_sum(av)), wave_sum(tree_sum(wv)), hn,
+                      cert_gamma(8 + tree_depth(kDnIters) + 6), out)) {
+        double acc = 0.0;
+#pragma unroll
+        for (int i = 0; i < kDnIters; ++i) acc = dot8_x(W[i], hv[i], acc);
+        out = bf16r((float)wave_sum64(acc));
+    }
     if (lane == 0) {
-        const float out = bf16r(d);
         P.x_out[n] = bf16r(P.x[n] + out);
         if (P.mlp_out) P.mlp_out[n] = (uint16_t)bf16_bits(out);
     }
