@@ -59,8 +59,10 @@ def parse_args():
 
 
 def cpu_baseline(blob, lay, x_tok: np.ndarray, budget_s: float, gpu_ids: np.ndarray):
-    """Oracle moe_layer per token on the host cores (experts pre-widened to
-    fp32 outside the timed region, as reference_decode's LayerWeights are)."""
+    """The reference's NumPy MoE layer per token on the host cores: the
+    oracle's fp32 restatement of reference_decode.py's arithmetic
+    (moe_layer_fp32; fp32 BLAS GEMVs, experts pre-widened to fp32 outside the
+    timed region, as reference_decode's LayerWeights are)."""
     sys.path.insert(0, str(ROOT))
     from fleet_moe.layout import view_u16
     from oracle import moe_oracle as orc
@@ -69,12 +71,12 @@ def cpu_baseline(blob, lay, x_tok: np.ndarray, budget_s: float, gpu_ids: np.ndar
                          shared=view_u16(blob, t["L1.shared"]), expert_stride=orc.HIDDEN * orc.MOE_INTER * 3,
                          norm=view_u16(blob, t["L1.norm_post"]))
     pl.widen()
-    orc.moe_layer(pl, x_tok[0])                      # warm-up call
+    orc.moe_layer_fp32(pl, x_tok[0])                 # warm-up call
     times, n_match = [], 0
     t_end = time.perf_counter() + budget_s
     for i in range(x_tok.shape[0]):
         t0 = time.perf_counter_ns()
-        r = orc.moe_layer(pl, x_tok[i])
+        r = orc.moe_layer_fp32(pl, x_tok[i])
         times.append((time.perf_counter_ns() - t0) / 1e3)
         n_match += int(np.array_equal(r["ids"], gpu_ids[i]))
         if time.perf_counter() > t_end:
@@ -91,7 +93,8 @@ def cpu_baseline(blob, lay, x_tok: np.ndarray, budget_s: float, gpu_ids: np.ndar
     return {
         "value": float(np.median(times)), "unit": "us/layer", "cores": cores, "kind": "port",
         "sample": f"{len(times)} of config 1's seeded tokens, one MoE layer each "
-                  f"(oracle/moe_oracle.moe_layer, NumPy {np.__version__}, BLAS threads = "
+                  f"(oracle/moe_oracle.moe_layer_fp32: reference_decode.py's fp32 NumPy "
+                  f"arithmetic, NumPy {np.__version__}, BLAS threads = "
                   f"{cores} visible cores, {cpu_model})",
         "ids_match_gpu": f"{n_match}/{len(times)}",
     }

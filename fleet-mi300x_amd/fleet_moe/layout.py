@@ -116,6 +116,43 @@ def parse_manifest(text: str):
     return scalars, tensors
 
 
+def layout_from_manifest(text: str) -> Layout:
+    """A Layout from a manifest's text: the tensors at their recorded offsets
+    (shape = flat bf16 elements; the manifest records bytes only) and the
+    scalars, so a blob packed by the reference (or by hf_pack) is addressed
+    exactly as the layouts built here."""
+    scalars, tensors = parse_manifest(text)
+    lay = Layout(scalars=dict(scalars))
+    end = 0
+    for name, (off, nbytes) in tensors.items():
+        if off % ALIGN:
+            raise ValueError(f"{name}: offset {off} is not {ALIGN}-byte aligned")
+        lay.tensors[name] = TensorEntry(name, off, nbytes, (nbytes // 2,))
+        end = max(end, off + nbytes)
+    lay.pos = end
+    return lay
+
+
+def load_packed(path, device="cuda", chunk_bytes: int = 1 << 28):
+    """Read a packed blob `path` (and `path`.manifest) into one uint8 device
+    tensor, streaming the file in chunks so the host never holds it whole.
+    Returns (blob tensor, Layout)."""
+    import torch
+    from pathlib import Path
+    path = Path(path)
+    lay = layout_from_manifest(Path(str(path) + ".manifest").read_text())
+    size = path.stat().st_size
+    if size < lay.nbytes:
+        raise ValueError(f"{path}: {size} bytes, manifest needs {lay.nbytes}")
+    blob = torch.empty(size, dtype=torch.uint8, device=device)
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    for a in range(0, size, chunk_bytes):
+        b = min(size, a + chunk_bytes)
+        blob[a:b].copy_(torch.from_numpy(np.array(mm[a:b])))
+    del mm
+    return blob, lay
+
+
 def moe_layout(dims: MoeDims = DSV2_LITE, layers=(1,), with_norm: bool = True) -> Layout:
     """Layout of the MoE tensors of `layers` (pack_weights.py:113-142 order:
     norm_post first, then router, experts, shared)."""

@@ -364,6 +364,45 @@ def moe_layer(layer: PackedLayer, x, top_k: int = TOP_K,
     return r
 
 
+def moe_layer_fp32(layer: PackedLayer, x, top_k: int = TOP_K,
+                   routed_scaling: float = ROUTED_SCALING, eps: float = RMS_EPS) -> dict:
+    """The MoE half of a decoder layer in the reference's own arithmetic: the
+    CPU path the benchmark times beside the GPU, not a checker.
+
+    reference_decode.py:262-287, 301-302 as written: fp32 NumPy/BLAS matmuls
+    for the router and every expert GEMV, SiLU x / (1 + exp(-x)) and the
+    softmax in fp32, bf16 rounding points as there, routed terms summed in
+    fp32 in selection order; the top-k set uses the lowest-index tie rule
+    (the reference's argpartition picks the same set and leaves the order of
+    equal scores unspecified). Experts come from layer.expert_f32 (pre-widened
+    by layer.widen(), as the reference's LayerWeights are fp32). Outputs agree
+    with moe_layer within bf16 tolerance (tests/test_oracle.py); ids agree
+    unless a 6th/7th-place gap is below fp32 resolution.
+    """
+    R = bf16_round
+    x = np.asarray(x, np.float32)
+    x_n = rms_norm(x, layer.gamma_f32(), eps)
+    logits = (layer.cache.get("router32") if "router32" in layer.cache
+              else layer.cache.setdefault("router32", layer.router_f32())) @ x_n
+    m = np.max(logits)
+    e = np.exp(logits - m)
+    scores = (e / np.sum(e)).astype(np.float32)
+    ids, pv = topk_lowest_index(scores, top_k)
+    ws = (pv * np.float32(routed_scaling)).astype(np.float32)
+
+    def mlp(g, u, d):
+        a = R(g @ x_n)
+        h = R(R(a / (np.float32(1.0) + np.exp(-a, dtype=np.float32))) * R(u @ x_n))
+        return R(d @ h)
+
+    y = np.zeros_like(x_n)
+    for k, eid in enumerate(ids):
+        y = y + R(ws[k] * mlp(*layer.expert_f32(int(eid))))
+    out = R(R(y) + mlp(*layer.shared_f32()))
+    return {"x_n": x_n, "logits": logits, "ids": ids, "weights": ws, "out": out,
+            "x_out": R(x + out)}
+
+
 def dense_layer(gate, up, down, x, gamma=None, eps: float = RMS_EPS) -> dict:
     """A dense decoder layer's FFN half: x' = bf16(x + mlp(rms_norm(x))).
 

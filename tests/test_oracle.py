@@ -390,6 +390,24 @@ def test_moe_matches_torch_hf_semantics_full_shape(full_layer):
         assert rel_err(r["out"], want[t]) <= 1e-2
 
 
+def test_moe_layer_fp32_reference_arithmetic_agrees(full_layer):
+    """The fp32 restatement the CPU baseline times (the reference's own BLAS
+    arithmetic) selects the same experts as the exact oracle and agrees with
+    it, and with the torch restatement of HF, within bf16 tolerance."""
+    _, _, pl = full_layer
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((3, 2048)).astype(np.float32)
+    want_hf, ti = hf_moe_bf16(pl, orc.rms_norm(x), top_k=6, scaling=1.0)
+    for t in range(3):
+        r = orc.moe_layer_fp32(pl, x[t])
+        e = orc.moe_layer(pl, x[t])
+        np.testing.assert_array_equal(r["ids"], e["ids"])
+        assert set(r["ids"].tolist()) == set(ti[t].tolist())
+        assert rel_err(r["out"], e["out"]) <= 1e-2
+        assert rel_err(r["out"], want_hf[t]) <= 1e-2
+        assert rel_err(r["x_out"], e["x_out"]) <= 1e-2
+
+
 def test_moe_grouped_equals_per_token_and_hf_rule():
     rng = np.random.default_rng(13)
     layer, _ = pack_tiny(rng, 64, 16, 8, 2, 0.08)
