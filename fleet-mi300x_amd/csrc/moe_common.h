@@ -195,6 +195,58 @@ __device__ __forceinline__ float wave_sum(float v) {
             __int_as_float(__builtin_amdgcn_readlane(b, 48)));
 }
 
+// Sum of lane l and lane l ^ 16 (permlane16_swap), then of l and l ^ 32
+// (permlane32_swap): the swap's two results hold both rows, so their sum is
+// the pair sum in every lane.
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+// N wave sums at once (N = 1, 2, 4, 8 or 16): lane l returns the sum over
+// all 64 lanes of v[l % N] (wave_msum below maps sums to lanes differently).
+// Each of the first log2 N levels halves the values a lane holds: it keeps
+// the half its lane bit k selects and adds the partner's copy of that half,
+// the partner being lane ^ 1, lane ^ 2 (quad permutes), then lane + 4 and
+// lane + 8 within the row of 16 (row rotates; the partner always has the
+// opposite bit k and the same lower bits, and the rotations cover every lane
+// of the row once). The remaining levels add the single value the same way,
+// then across rows and halves. N sums cost about 3N + 10 instructions
+// instead of N full reductions, and each result is a binary tree of 63 fp32
+// additions, six roundings deep.
+template <int K, int N>
+__device__ __forceinline__ void nsum_level(float (&v)[N], int lane) {
+    constexpr int kCtrl = K == 0 ? 0xB1 : K == 1 ? 0x4E : K == 2 ? 0x124 : 0x128;
+    constexpr int n = N >> K;                 // values held entering level K
+    if constexpr (n > 1) {
+        const bool bit = (lane >> K) & 1;
+#pragma unroll
+        for (int i = 0; i < n / 2; ++i) {
+            const float keep = bit ? v[2 * i + 1] : v[2 * i];
+            const float send = bit ? v[2 * i] : v[2 * i + 1];
+            v[i] = keep + __int_as_float(FLEET_DPP(__float_as_int(send), kCtrl));
+        }
+    } else {
+        v[0] += __int_as_float(FLEET_DPP(__float_as_int(v[0]), kCtrl));
+    }
+}
+template <int N>
+__device__ __forceinline__ float wave_nsum(float (&v)[N]) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "N sums, N a power of 2 <= 16");
+    const int lane = threadIdx.x & 63;
+    nsum_level<0>(v, lane);
+    nsum_level<1>(v, lane);
+    nsum_level<2>(v, lane);
+    nsum_level<3>(v, lane);
+    return xor32_sum(xor16_sum(v[0]));
+}
+
 template <int kCtrl>
 __device__ __forceinline__ double dpp64(double v) {
     const long long b = __double_as_longlong(v);

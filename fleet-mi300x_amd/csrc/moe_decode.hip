@@ -266,36 +266,42 @@ __device__ bool select_routing(const Params& P, Lds& L, uint32_t epoch, float xn
     return true;
 }
 
-// Exact weights and order for a locally selected set: softmax of the exact
-// logits (fp64, as the standalone router computes it), then each slot's
-// weight and the slots sorted by (p descending, id ascending). Also checks
-// that the set is the exact top 6.
-__device__ void exact_weights(const Params& P, Lds& L, uint32_t epoch) {
+// Exact weights and order for a locally selected set, from the exact logit
+// of this lane's expert: softmax (fp64, as the standalone router computes
+// it), then each slot's weight and the slots sorted by (p descending, id
+// ascending), one ballot per slot. Also checks that the set is the exact
+// top 6.
+__device__ void exact_weights_from(const Params& P, Lds& L, float el) {
     const int lane = threadIdx.x & (kLanes - 1);
-    float el;
-    if (!poll_exact_logits(P, epoch, el)) return;
     const float m = wave_max(el);
     const double e = exp((double)el - (double)m);
     const double sum = wave_sum64(e);
     const float p = (float)(e / sum);
-    const int pb = __float_as_int(p);
-    // rank of this lane's expert among all 64 by (p desc, index asc)
-    int rank = 0;
-#pragma unroll 8
-    for (int j = 0; j < kLanes; ++j) {
-        const float o = __int_as_float(__builtin_amdgcn_readlane(pb, j));
-        rank += (o > p) || (o == p && j < lane);
+    float pk = 0.f;
+    int rk = 0;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        const int id = wave_bcast(L.ids[k]);
+        const float q = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), id));
+        const int rank = __popcll(__ballot(p > q || (p == q && lane < id)));
+        pk = lane == k ? q : pk;
+        rk = lane == k ? rank : rk;
     }
-    // every lane takes part in the permutes; lanes < 6 use the result
-    const int id = lane < kTopK ? L.ids[lane] : 0;
-    const float pk = __int_as_float(__builtin_amdgcn_ds_bpermute(id << 2, pb));
-    const int rk = __builtin_amdgcn_ds_bpermute(id << 2, rank);
     if (lane < kTopK) {
         L.w[lane] = pk * P.scaling;
         if (rk < kTopK) L.order[rk] = lane;
         else __hip_atomic_fetch_or(&P.ws->abort, kAbortRouteMismatch, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+// One poll of this lane's exact router word (tag = epoch in the high half).
+__device__ __forceinline__ uint64_t ld_exact_logit(const Params& P) {
+    return __hip_atomic_load(&P.ws->logit[threadIdx.x & (kLanes - 1)], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ void exact_weights(const Params& P, Lds& L, uint32_t epoch) {
+    float el;
+    if (poll_exact_logits(P, epoch, el)) exact_weights_from(P, L, el);
 }
 
 // Base of gate/up row pair `pair` of `unit`, as 16-byte chunks. ids are in
@@ -327,7 +333,9 @@ __device__ __forceinline__ float exact_row2048(const u32x4* w, const u32x4 (&xq)
 // Reduce one gate/up pair and publish its tagged h word. bf16(g) and bf16(u)
 // are the exactly rounded values: the fp32 evaluation (four v_dot2 chains of
 // depth 8, a two-level tree, the wave sum: 16 roundings) is certified against
-// ||w|| ||x_norm||, and a row near a bf16 boundary is evaluated exactly.
+// ||w|| ||x_norm||, and a row near a bf16 boundary is evaluated exactly. The
+// four sums (g, u, |g row|^2, |u row|^2) are reduced together into lanes
+// 0..3; lanes 0 and 1 certify g and u.
 __device__ __forceinline__ void finish_pair(const Params& P, int unit, int pair,
                                             const u32x4 (&b)[8], const u32x4 (&xq)[4],
                                             uint32_t tag, float xnorm) {
@@ -340,16 +348,24 @@ __device__ __forceinline__ void finish_pair(const Params& P, int unit, int pair,
         gw[m] = dot8_d2(b[m], b[m], 0.f);
         uw[m] = dot8_d2(b[4 + m], b[4 + m], 0.f);
     }
-    const float gs = wave_sum((g[0] + g[1]) + (g[2] + g[3]));
-    const float us = wave_sum((u[0] + u[1]) + (u[2] + u[3]));
-    const float gws = wave_sum((gw[0] + gw[1]) + (gw[2] + gw[3]));
-    const float uws = wave_sum((uw[0] + uw[1]) + (uw[2] + uw[3]));
-    const float gam = cert_gamma(16);
-    float gb, ub;
-    if (!certify_bf16(gs, gws, xnorm, gam, gb)) gb = bf16r(exact_row2048(b, xq));
-    if (!certify_bf16(us, uws, xnorm, gam, ub)) ub = bf16r(exact_row2048(b + 4, xq));
+    float v[4] = {(g[0] + g[1]) + (g[2] + g[3]), (u[0] + u[1]) + (u[2] + u[3]),
+                  (gw[0] + gw[1]) + (gw[2] + gw[3]), (uw[0] + uw[1]) + (uw[2] + uw[3])};
+    const float s = wave_nsum(v);                  // lane % 4: g, u, gw, uw
+    const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x4E));   // lane ^ 2
+    float r;
+    const bool ok = certify_bf16(s, w2, xnorm, cert_gamma(16), r);
+    const uint64_t bad = __ballot(!ok) & 3ull;
+    if (bad & 1ull) {
+        const float e = bf16r(exact_row2048(b, xq));
+        r = lane == 0 ? e : r;
+    }
+    if (bad & 2ull) {
+        const float e = bf16r(exact_row2048(b + 4, xq));
+        r = lane == 1 ? e : r;
+    }
+    const float ub = __int_as_float(FLEET_DPP(__float_as_int(r), 0xB1));   // lane ^ 1
     if (lane == 0) {
-        const float h = bf16r(bf16r(silu_rn(gb)) * ub);
+        const float h = bf16r(bf16r(silu_rn(r)) * ub);
         st_agent(&P.ws->h[h_offset(unit) + pair], tag | bf16_bits(h));
     }
 }
@@ -491,9 +507,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     FLEET_TRACE(1);
 
     // a2 (local): eight router rows per wave, dot2 with fp32 accumulation,
-    // plus each row's sum of squares for the error bound.
+    // plus each row's sum of squares for the error bound; the 16 sums are
+    // reduced together, lane r < 8 ending with row r's logit and lane 8 + r
+    // with its sum of squares.
     {
-        float lg[8], nr[8];
+        float v[16];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             float a = 0.f, n = 0.f;
@@ -502,8 +520,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
                 a = dot8_d2(ra[r][m], xq[m], a);
                 n = dot8_d2(ra[r][m], ra[r][m], n);
             }
-            lg[r] = wave_sum(a);
-            nr[r] = wave_sum(n);
+            v[r] = a;
+            v[8 + r] = n;
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -513,19 +531,12 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
                 a = dot8_d2(rb[r][m], xq[m], a);
                 n = dot8_d2(rb[r][m], rb[r][m], n);
             }
-            lg[4 + r] = wave_sum(a);
-            nr[4 + r] = wave_sum(n);
+            v[4 + r] = a;
+            v[12 + r] = n;
         }
-        if (lane < kRouterRowsPerWave) {
-            float lv = lg[0], nv = nr[0];
-#pragma unroll
-            for (int r = 1; r < 8; ++r) {
-                lv = lane == r ? lg[r] : lv;
-                nv = lane == r ? nr[r] : nv;
-            }
-            L.llog[rrow0 + lane] = lv;
-            L.lnrm[rrow0 + lane] = nv;
-        }
+        const float s = wave_nsum(v);
+        if (lane < kRouterRowsPerWave) L.llog[rrow0 + lane] = s;
+        else if (lane < 2 * kRouterRowsPerWave) L.lnrm[rrow0 + lane - kRouterRowsPerWave] = s;
     }
 
     __syncthreads();
@@ -549,7 +560,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         item_of(wg, item, u, p);
         finish_pair(P, u, p, b, xq, tag, xnorm);
     };
-    bool exact_sel = false;
+    bool exact_sel = false, weights_pending = false;
+    uint64_t ew = 0;
     cur = ctl ? -1 : wave;
     if (ctl) {
         __builtin_amdgcn_s_setprio(2);
@@ -577,15 +589,29 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
             for (int k = 0; k < kSharedBlockBytes / 1024; ++k)
                 __builtin_amdgcn_global_load_lds(src + k * 1024, L.sdown + k * 1024, 16, 0, 0);
         }
+        weights_pending = ok && !exact_sel;
         cur = claim();
+        if (weights_pending) ew = ld_exact_logit(P);
         if (cur >= 0) issue(cur, bufA);
     }
     FLEET_TRACE(2);
 
-    // Phase G: gate/up pairs, one in flight per streaming wave.
+    // Phase G: gate/up pairs, one in flight per streaming wave. The control
+    // wave also polls the exact router logits (for the weights of a locally
+    // selected set) as soon as they may be published: each poll is issued
+    // just before a pair's loads, so the pair's wait covers it and the wave
+    // never stalls on it alone.
     while (cur >= 0) {
         const int nxt = claim();
         finish(cur, bufA);
+        if (weights_pending) {
+            if (__all((uint32_t)(ew >> 32) == epoch)) {
+                exact_weights_from(P, L, __uint_as_float((uint32_t)ew));
+                weights_pending = false;
+            } else if (nxt >= 0) {
+                ew = ld_exact_logit(P);
+            }
+        }
         if (nxt >= 0) issue(nxt, bufA);
         cur = nxt;
     }
@@ -616,39 +642,50 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         u32x4 H[3];
         wait_h<3>(P, unit, kInterChunks, tag, H);
         FLEET_TRACE(5);
-        const float hn = __builtin_sqrtf(wave_sum((dot8_d2(H[0], H[0], 0.f) +
-                                                   dot8_d2(H[1], H[1], 0.f)) +
-                                                  dot8_d2(H[2], H[2], 0.f))) * 1.0001f;
-        const float gam = cert_gamma(16);     // v_dot2 chain 8, tree 2, wave sum 6
+        float hv[1] = {(dot8_d2(H[0], H[0], 0.f) + dot8_d2(H[1], H[1], 0.f)) +
+                       dot8_d2(H[2], H[2], 0.f)};
+        const float hn = __builtin_sqrtf(wave_nsum(hv)) * 1.0001f;
+        // the 8 rows' dots and sums of squares reduced together: lane r < 8
+        // holds row r's dot, lane 8 + r its sum of squares
+        float v[16];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const u32x4* w = &W[3 * r];
-            const float a = wave_sum((dot8_d2(w[0], H[0], 0.f) + dot8_d2(w[1], H[1], 0.f)) +
-                                     dot8_d2(w[2], H[2], 0.f));
-            const float n = wave_sum((dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) +
-                                     dot8_d2(w[2], w[2], 0.f));
-            float d;
-            if (!certify_bf16(a, n, hn, gam, d)) {
-                double acc = 0.0;
-#pragma unroll
-                for (int m = 0; m < 3; ++m) acc = dot8_x(w[m], H[m], acc);
-                d = bf16r((float)wave_sum64(acc));
-            }
-            if (lane == 0) L.part[unit][r] = d;
+            v[r] = (dot8_d2(w[0], H[0], 0.f) + dot8_d2(w[1], H[1], 0.f)) +
+                   dot8_d2(w[2], H[2], 0.f);
+            v[8 + r] = (dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) +
+                       dot8_d2(w[2], w[2], 0.f);
         }
+        const float s = wave_nsum(v);
+        const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x128));   // lane + 8
+        float d;
+        const bool ok = certify_bf16(s, w2, hn, cert_gamma(16), d);  // v_dot2 chain 8, tree 2, sum 6
+        const uint64_t bad = __ballot(!ok) & 0xffull;
+        if (bad) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                if (bad & (1ull << r)) {
+                    double acc = 0.0;
+#pragma unroll
+                    for (int m = 0; m < 3; ++m) acc = dot8_x(W[3 * r + m], H[m], acc);
+                    const float e = bf16r((float)wave_sum64(acc));
+                    d = lane == r ? e : d;
+                }
+            }
+        }
+        if (lane < kRowsPerWG) L.part[unit][lane] = d;
     } else {
         if (ctl) {
-            // exact weights and order (the exact logits were published early)
-            if (!exact_sel && __hip_atomic_load(&L.route, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_WORKGROUP) == 2)
-                exact_weights(P, L, epoch);
-            FLEET_TRACE(9);
             // the shared down rows this wave put in flight at the start
             __builtin_amdgcn_s_waitcnt(0x0F70);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             if (lane == 0)
                 __hip_atomic_store(&L.sdown_ready, 1, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+            // exact weights and order, if phase G ended before the exact
+            // logits were seen (they are needed only by the final combine)
+            if (weights_pending) exact_weights(P, L, epoch);
+            FLEET_TRACE(9);
         } else {
             while (__hip_atomic_load(&L.sdown_ready, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
@@ -663,10 +700,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         float hq[6];
 #pragma unroll
         for (int m = 0; m < 6; ++m) hq[m] = dot8_d2(H[m], H[m], 0.f);
-        const float hn =
-            __builtin_sqrtf(wave_sum(((hq[0] + hq[1]) + (hq[2] + hq[3])) + (hq[4] + hq[5]))) *
-            1.0001f;
-        const float gam = cert_gamma(17);     // v_dot2 chain 8, tree 3, wave sum 6
+        float hv[1] = {((hq[0] + hq[1]) + (hq[2] + hq[3])) + (hq[4] + hq[5])};
+        const float hn = __builtin_sqrtf(wave_nsum(hv)) * 1.0001f;
+        // the 4 rows' dots and sums of squares reduced together: lane r < 4
+        // holds row rs + r's dot, lane 4 + r its sum of squares
+        float v[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const u32x4* wr = reinterpret_cast<const u32x4*>(L.sdown + (rs + r) * kSharedRowBytes);
@@ -682,17 +720,33 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
                 av[m] = dot8_d2(w[m], H[m], 0.f);
                 nv[m] = dot8_d2(w[m], w[m], 0.f);
             }
-            const float a = wave_sum(((av[0] + av[1]) + (av[2] + av[3])) + (av[4] + av[5]));
-            const float n = wave_sum(((nv[0] + nv[1]) + (nv[2] + nv[3])) + (nv[4] + nv[5]));
-            float d;
-            if (!certify_bf16(a, n, hn, gam, d)) {
-                double acc = 0.0;
-#pragma unroll
-                for (int m = 0; m < 6; ++m) acc = dot8_x(w[m], H[m], acc);
-                d = bf16r((float)wave_sum64(acc));
-            }
-            if (lane == 0) L.part[0][rs + r] = d;
+            v[r] = ((av[0] + av[1]) + (av[2] + av[3])) + (av[4] + av[5]);
+            v[4 + r] = ((nv[0] + nv[1]) + (nv[2] + nv[3])) + (nv[4] + nv[5]);
         }
+        const float s = wave_nsum(v);
+        const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x124));   // lane + 4
+        float d;
+        const bool ok = certify_bf16(s, w2, hn, cert_gamma(17), d);  // v_dot2 chain 8, tree 3, sum 6
+        const uint64_t bad = __ballot(!ok) & 0xfull;
+        if (bad) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (bad & (1ull << r)) {
+                    const u32x4* wr =
+                        reinterpret_cast<const u32x4*>(L.sdown + (rs + r) * kSharedRowBytes);
+                    double acc = 0.0;
+#pragma unroll
+                    for (int m = 0; m < 6; ++m) {
+                        const int c = lane + kLanes * m;
+                        const u32x4 w = c < kSharedChunks ? wr[c] : u32x4{0u, 0u, 0u, 0u};
+                        acc = dot8_x(w, H[m], acc);
+                    }
+                    const float e = bf16r((float)wave_sum64(acc));
+                    d = lane == r ? e : d;
+                }
+            }
+        }
+        if (lane < 4) L.part[0][rs + lane] = d;
     }
     FLEET_TRACE(6);
     __syncthreads();
