@@ -421,7 +421,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     __shared__ Lds L;
     const int wg = blockIdx.x;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: branches on it are scalar
     const int lane = tid & (kLanes - 1);
     Workspace* ws = P.ws;
     const bool ctl = wave == kCtlWave;

@@ -142,7 +142,9 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     while (cur >= 0) {
         const int nxt = claim();
         // bf16(g), bf16(u) exactly rounded: certified fp32 evaluation (depth
-        // 8 + 2 + 6), the exact fp64 sum for a row the bound cannot decide
+        // 8 + 2 + 6), the exact fp64 sum for a row the bound cannot decide.
+        // The four sums (g, u, |g row|^2, |u row|^2) are reduced together
+        // into lanes 0..3; lanes 0 and 1 certify g and u.
         float g[4], u[4], gw[4], uw[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -151,22 +153,25 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
             gw[m] = dot8_d2(buf[m], buf[m], 0.f);
             uw[m] = dot8_d2(buf[4 + m], buf[4 + m], 0.f);
         }
-        const float gam = cert_gamma(16);
-        float gb, ub;
-        if (!certify_bf16(wave_sum(tree_sum(g)), wave_sum(tree_sum(gw)), xnorm, gam, gb)) {
-            double a = 0.0;
+        float v4[4] = {tree_sum(g), tree_sum(u), tree_sum(gw), tree_sum(uw)};
+        const float s = wave_nsum(v4);                                         // lane % 4: g, u, gw, uw
+        const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x4E));   // lane ^ 2
+        float r;
+        const bool okc = certify_bf16(s, w2, xnorm, cert_gamma(16), r);
+        const uint64_t bad = __ballot(!okc) & 3ull;
 #pragma unroll
-            for (int m = 0; m < 4; ++m) a = dot8_x(buf[m], xq[m], a);
-            gb = bf16r((float)wave_sum64(a));
-        }
-        if (!certify_bf16(wave_sum(tree_sum(u)), wave_sum(tree_sum(uw)), xnorm, gam, ub)) {
-            double a = 0.0;
+        for (int q = 0; q < 2; ++q) {
+            if (bad & (1ull << q)) {
+                double a = 0.0;
 #pragma unroll
-            for (int m = 0; m < 4; ++m) a = dot8_x(buf[4 + m], xq[m], a);
-            ub = bf16r((float)wave_sum64(a));
+                for (int m = 0; m < 4; ++m) a = dot8_x(buf[4 * q + m], xq[m], a);
+                const float e = bf16r((float)wave_sum64(a));
+                r = lane == q ? e : r;
+            }
         }
+        const float ub = __int_as_float(FLEET_DPP(__float_as_int(r), 0xB1));   // lane ^ 1
         if (lane == 0) {
-            const float h = bf16r(bf16r(silu_rn(gb)) * ub);
+            const float h = bf16r(bf16r(silu_rn(r)) * ub);
             st_agent(&ws->h[wg + kWG * cur], tag | bf16_bits(h));
         }
         if (nxt >= 0) issue_pair(gu + (int64_t)(wg + kWG * nxt) * 2 * kRowChunks, lane, buf);
@@ -218,10 +223,17 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
         wv[i] = dot8_d2(W[i], W[i], 0.f);
         hq[i] = dot8_d2(hv[i], hv[i], 0.f);
     }
-    const float hn = __builtin_sqrtf(wave_sum(tree_sum(hq))) * 1.0001f;
+    // the three sums reduced together: lane % 4 = 0, 1, 2 holds the dot,
+    // the row's and h's sums of squares; every lane of a quad takes all three
+    // (the same bits in every quad, so every lane decides alike)
+    float v4[4] = {tree_sum(av), tree_sum(wv), tree_sum(hq), 0.f};
+    const float s = wave_nsum(v4);
+    const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x55));   // quad lane 1
+    const float h2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0xAA));   // quad lane 2
+    const float a0 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x00));   // quad lane 0
+    const float hn = __builtin_sqrtf(h2) * 1.0001f;
     float out;
-    if (!certify_bf16(wave_sum(tree_sum(av)), wave_sum(tree_sum(wv)), hn,
-                      cert_gamma(8 + tree_depth(kDnIters) + 6), out)) {
+    if (!certify_bf16(a0, w2, hn, cert_gamma(8 + tree_depth(kDnIters) + 6), out)) {
         double acc = 0.0;
 #pragma unroll
         for (int i = 0; i < kDnIters; ++i) acc = dot8_x(W[i], hv[i], acc);
