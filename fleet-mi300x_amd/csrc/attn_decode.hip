@@ -182,6 +182,40 @@ __device__ __forceinline__ float dot_row_bf16(const u32x4 (&w)[4], const u32x4 (
     return r;
 }
 
+// Two rows at once (the second only if `two`): their dots and sums of
+// squares reduced together (lane % 4: a0, a1, n0, n1), lanes 0 and 1
+// certify, a row the bound cannot decide is evaluated exactly. r0 / r1
+// receive the exactly rounded bf16 results in every lane.
+__device__ __forceinline__ void dot_rows2_bf16(const u32x4 (&w0)[4], const u32x4 (&w1)[4],
+                                               bool two, const u32x4 (&xq)[4], float xnorm,
+                                               float& r0, float& r1) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    float a0[4], a1[4], n0[4], n1[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        a0[m] = dot8_d2(w0[m], xq[m], 0.f);
+        a1[m] = dot8_d2(w1[m], xq[m], 0.f);
+        n0[m] = dot8_d2(w0[m], w0[m], 0.f);
+        n1[m] = dot8_d2(w1[m], w1[m], 0.f);
+    }
+    float v[4] = {tree_sum(a0), tree_sum(a1), tree_sum(n0), tree_sum(n1)};
+    const float sv = wave_nsum(v);
+    const float w2 = __int_as_float(FLEET_DPP(__float_as_int(sv), 0x4E));   // lane ^ 2
+    float r;
+    const bool ok = certify_bf16(sv, w2, xnorm, cert_gamma(16), r);
+    const uint64_t bad = __ballot(!ok) & (two ? 3ull : 1ull);
+    if (bad & 1ull) {
+        const float e = bf16r(dot_row(w0, xq));
+        r = lane == 0 ? e : r;
+    }
+    if (bad & 2ull) {
+        const float e = bf16r(dot_row(w1, xq));
+        r = lane == 1 ? e : r;
+    }
+    r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
+    r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 1));
+}
+
 // Sum over the 8 lanes of each aligned group of 8 (quad exchanges, then the
 // half-row mirror); every lane of the group returns the group total.
 __device__ __forceinline__ double sum8_lanes(double v) {
@@ -223,6 +257,27 @@ __device__ __forceinline__ double msum_xchg64(double x) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+// x plus its step-K partner's x. The cross-row steps (K = 4: lane ^ 16,
+// K = 5: lane ^ 32) go through permlane swaps of both halves: the swap's two
+// results hold the lane's own value and its partner's, in an order that
+// depends on the row, and their sum is the same either way.
+template <int K>
+__device__ __forceinline__ double msum_pair64(double x) {
+    if constexpr (K >= 4) {
+        const long long b = __double_as_longlong(x);
+        const uint32_t lo = (uint32_t)(b & 0xffffffffll), hi = (uint32_t)(b >> 32);
+        const auto sl = K == 4 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                               : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto sh = K == 4 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                               : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        const double a = __longlong_as_double((long long)(((uint64_t)sh[0] << 32) | sl[0]));
+        const double c = __longlong_as_double((long long)(((uint64_t)sh[1] << 32) | sl[1]));
+        return a + c;
+    } else {
+        return x + msum_xchg64<K>(x);
+    }
+}
+
 template <int K, int LEN, int N>
 __device__ __forceinline__ void msum_step64(double (&v)[N]) {
     if constexpr (K < 6) {
@@ -230,13 +285,13 @@ __device__ __forceinline__ void msum_step64(double (&v)[N]) {
             const bool up = __builtin_popcount((threadIdx.x & (kLanes - 1)) & kMsumDual[K]) & 1;
 #pragma unroll
             for (int j = 0; j < LEN / 2; ++j) {
-                const double lo = v[j] + msum_xchg64<K>(v[j]);
-                const double hi = v[j + LEN / 2] + msum_xchg64<K>(v[j + LEN / 2]);
+                const double lo = msum_pair64<K>(v[j]);
+                const double hi = msum_pair64<K>(v[j + LEN / 2]);
                 v[j] = up ? hi : lo;
             }
             msum_step64<K + 1, LEN / 2, N>(v);
         } else {
-            v[0] += msum_xchg64<K>(v[0]);
+            v[0] = msum_pair64<K>(v[0]);
             msum_step64<K + 1, 1, N>(v);
         }
     }
@@ -434,7 +489,8 @@ struct Lds {
 
 __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     __shared__ Lds L;
-    const int wg = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
+    const int wg = blockIdx.x, tid = threadIdx.x, lane = tid & (kLanes - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: branches on it are scalar
     Workspace* ws = P.ws;
     const int pos = P.pos_dev ? *P.pos_dev : P.pos_host;
     if (pos < 0 || pos >= P.max_pos) {
@@ -463,7 +519,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     const int r1 = wg + kWG * (wave + kWaves);            // valid below 3648
     u32x4 wq0[4], wq1[4];
     load_row(P.qkv, r0, wq0);
-    if (r1 < kQkvRows) load_row(P.qkv, r1, wq1);
+    if (r1 < kQkvRows) {
+        load_row(P.qkv, r1, wq1);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) wq1[m] = u32x4{0u, 0u, 0u, 0u};
+    }
     ATTN_TRACE(1);
     // ---- S1: RMSNorm, then this wave's rows of [q_proj ; kv_a]
     const float xnorm = norm2048(xv, gb, P.eps, L.xb, L.red);
@@ -472,14 +533,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         u32x4 xq[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(L.xb)[lane + kLanes * m];
-        const float a0 = dot_row_bf16(wq0, xq, xnorm);
+        const bool two = r1 < kQkvRows;
+        float a0, a1;
+        dot_rows2_bf16(wq0, wq1, two, xq, xnorm, a0, a1);
         if (lane == 0) {
             ws->qkv[r0] = a0;
             st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
-        }
-        if (r1 < kQkvRows) {
-            const float a1 = dot_row_bf16(wq1, xq, xnorm);
-            if (lane == 0) {
+            if (two) {
                 ws->qkv[r1] = a1;
                 st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
             }
@@ -820,25 +880,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     }
 }
 
-// Rows first, first + stride, ... (< end) of a K = 2048 matrix against the
-// packed bf16 vector xq (2-norm xnorm); each wave keeps its next row in
-// flight while it reduces the current one. f(row, value) receives every
-// row's exactly rounded bf16 result.
-template <typename F>
-__device__ __forceinline__ void gemv_rows2048(const uint16_t* W, int first, int stride, int end,
-                                              const u32x4 (&xq)[4], float xnorm, F f) {
-    if (first >= end) return;
-    u32x4 w[4], wn[4];
-    load_row(W, first, w);
-    for (int row = first; row < end; row += stride) {
-        const int nxt = row + stride;
-        if (nxt < end) load_row(W, nxt, wn);
-        f(row, dot_row_bf16(w, xq, xnorm));
-#pragma unroll
-        for (int m = 0; m < 4; ++m) w[m] = wn[m];
-    }
-}
-
 // ---------------------------------------------------------------- embed / lm_head / argmax
 __global__ __launch_bounds__(kThreads, 1) void embed_kernel(const uint16_t* E, const int32_t* token,
                                                             float* x, Workspace* ws) {
@@ -870,16 +911,45 @@ __global__ __launch_bounds__(kThreads, 1) void lmhead_kernel(const float* x, con
     u32x4 xq[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xq[m] = reinterpret_cast<const u32x4*>(xb)[lane + kLanes * m];
-    float bv = -INFINITY;
+    // This wave's rows first + stride i (i < 50), two at a time from two
+    // buffers in turn (each wait is for the older pair while the newer one
+    // streams); lane i keeps row i's logit until the one store at the end,
+    // since a store among the loads would make every wait a full drain.
+    constexpr int kRowsPerWave = kVocab / (kWG * kWaves);   // 50
+    constexpr int kPairsPerWave = kRowsPerWave / 2;          // 25
+    static_assert(kVocab % (kWG * kWaves) == 0 && kRowsPerWave % 2 == 0 &&
+                      kPairsPerWave % 2 == 1 && kRowsPerWave <= kLanes,
+                  "lm_head rows: 25 pairs per wave, the last in buffer A");
+    const int first = blockIdx.x + kWG * wave, stride = kWG * kWaves;
+    float bv = -INFINITY, lg = 0.f;
     int bi = 0x7fffffff;
-    gemv_rows2048(W, blockIdx.x + kWG * wave, kWG * kWaves, kVocab, xq, xnorm,
-                  [&](int row, float v) {
-        if (logits && lane == 0) logits[row] = v;
-        if (v > bv || (v == bv && row < bi)) {
-            bv = v;
-            bi = row;
-        }
-    });
+    auto take = [&](int i, float v0, float v1) {
+        lg = lane == i ? v0 : lg;
+        lg = lane == i + 1 ? v1 : lg;
+        const int row = first + stride * i;
+        if (v0 > bv) { bv = v0; bi = row; }        // rows ascend: ties keep the lower
+        if (v1 > bv) { bv = v1; bi = row + stride; }
+    };
+    u32x4 a0[4], a1[4], b0[4], b1[4];
+    load_row(W, first, a0);
+    load_row(W, first + stride, a1);
+    for (int p = 0; p + 1 < kPairsPerWave; p += 2) {
+        load_row(W, first + stride * (2 * p + 2), b0);
+        load_row(W, first + stride * (2 * p + 3), b1);
+        float v0, v1;
+        dot_rows2_bf16(a0, a1, true, xq, xnorm, v0, v1);
+        take(2 * p, v0, v1);
+        load_row(W, first + stride * (2 * p + 4), a0);
+        load_row(W, first + stride * (2 * p + 5), a1);
+        dot_rows2_bf16(b0, b1, true, xq, xnorm, v0, v1);
+        take(2 * p + 2, v0, v1);
+    }
+    {
+        float v0, v1;
+        dot_rows2_bf16(a0, a1, true, xq, xnorm, v0, v1);
+        take(kRowsPerWave - 2, v0, v1);
+    }
+    if (logits && lane < kRowsPerWave) logits[first + stride * lane] = lg;
     if (lane == 0) {
         bv_s[wave] = bv;
         bi_s[wave] = bi;

@@ -326,7 +326,7 @@ __device__ __forceinline__ u32x4 ld_dev16(__amdgpu_buffer_rsrc_t r, int byte_off
 // Multi-value wave reduction: N values per lane (N a power of two <= 64) are
 // summed over the 64 lanes in six exchange steps, lane L with lane L ^ a_k for
 // a = {1, 2, 7, 15, 16, 32} (DPP quad_perm x2, row_half_mirror, row_mirror,
-// ds_swizzle, ds_bpermute). In each of the first log2(N) steps a lane keeps
+// then permlane16 / permlane32 swaps). In each of the first log2(N) steps a lane keeps
 // half of its values (the upper half when parity(L & f_k) = 1, f = {5, 6, 12,
 // 8, 16, 32}, the dual basis of a) and adds its partner's copy of that half;
 // the remaining steps add the single value. On return v[0] of every lane holds
@@ -347,6 +347,14 @@ __device__ __forceinline__ float msum_xchg(float x) {
 }
 constexpr int kMsumDual[6] = {5, 6, 12, 8, 16, 32};
 
+// x plus its step-K partner's x (the cross-row steps through permlane swaps).
+template <int K>
+__device__ __forceinline__ float msum_pair(float x) {
+    if constexpr (K == 4) return xor16_sum(x);
+    else if constexpr (K == 5) return xor32_sum(x);
+    else return x + msum_xchg<K>(x);
+}
+
 template <int K, int LEN, int N>
 __device__ __forceinline__ void msum_step(float (&v)[N]) {
     if constexpr (K < 6) {
@@ -354,13 +362,13 @@ __device__ __forceinline__ void msum_step(float (&v)[N]) {
             const bool up = __builtin_popcount((threadIdx.x & (kLanes - 1)) & kMsumDual[K]) & 1;
 #pragma unroll
             for (int j = 0; j < LEN / 2; ++j) {
-                const float lo = v[j] + msum_xchg<K>(v[j]);
-                const float hi = v[j + LEN / 2] + msum_xchg<K>(v[j + LEN / 2]);
+                const float lo = msum_pair<K>(v[j]);
+                const float hi = msum_pair<K>(v[j + LEN / 2]);
                 v[j] = up ? hi : lo;
             }
             msum_step<K + 1, LEN / 2, N>(v);
         } else {
-            v[0] += msum_xchg<K>(v[0]);
+            v[0] = msum_pair<K>(v[0]);
             msum_step<K + 1, 1, N>(v);
         }
     }
