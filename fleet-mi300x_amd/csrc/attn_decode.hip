@@ -20,7 +20,9 @@
 // are published, and every weight slice and cache row a workgroup will need
 // is put in flight at the start, before the first wait:
 //   S1 qkv    RMSNorm(x) in every workgroup, then the 3648 rows of
-//             [q_proj ; kv_a]: row r in workgroup r % 256, wave (r / 256) % 8.
+//             [q_proj ; kv_a]: head h's 192 q rows in its 16 workgroups
+//             (row 192 h + k + 16 i in workgroup (h, k)), kv_a row 3072 + j
+//             in workgroup j % 256.
 //   S2 q_c    workgroup (h, k): columns 32k .. 32k+31 of head h's absorbed
 //             query q_c = W_UK^T q_nope (128 rows x 32 columns of W_UK).
 //   S3 mla    workgroup (h, k): positions chunk k of head h (16 chunks of
@@ -32,9 +34,13 @@
 //             chunk partials and rounded once; then rows 8k .. 8k+7 of
 //             W_UV o_c, bf16.
 //   S5 oproj  workgroup w: rows 8w .. 8w+7 of o_proj, bf16, residual add.
-// Workgroup w has (h, k) = ((w / 8) % 16, w % 8 + 8 (w / 128)): the 16 heads
-// of one position chunk share an XCD (w % 8), so each XCD's L2 reads its two
-// chunks of the cache once.
+// Workgroup w has (h, k) = (w % 8 + 8 ((w / 8) % 2), w / 16): workgroups are
+// dealt to the 8 XCDs round-robin (w % 8), so all 16 workgroups of a head
+// share one XCD and its L2. Everything that passes between the workgroups of
+// one head (its q rows, q_c, the chunk partials, o_c) is stored into that L2
+// only (workgroup-scope stores) and found there by the device-scope polls;
+// only kv_a (every head needs the new cache row) and the head outputs
+// (o_proj needs all of them) are written through to memory.
 // The position can come from the host (an argument) or from device memory
 // (pos_dev), so a whole decode step can be captured once in a HIP graph and
 // replayed: the argmax kernel then advances *pos_dev itself. A device
@@ -376,6 +382,11 @@ __device__ __forceinline__ bool tagged(const u32x4& v, uint32_t tag) {
 // runs out (or finds the sticky status set by another wait) raises
 // FLEET_MOE_ABORT_ATTN_WAIT and returns false; the caller carries on with
 // whatever was read, so the grid always drains.
+// Polls are device-scope loads, which are served by the XCD's own L2 when
+// it holds the line. XCD-local words (producer and consumer on one XCD) are
+// stored at workgroup scope: the store stops in that L2 instead of writing
+// through to memory, and a consumer on the same XCD sees it about half a
+// round trip sooner (a consumer on another XCD would not see it at all).
 __device__ bool poll16(const void* base, int off, bool active, uint32_t tag, u32x4& v,
                        Workspace* ws) {
     const __amdgpu_buffer_rsrc_t r = rsrc(base);
@@ -409,18 +420,26 @@ __device__ __forceinline__ float tagged_f32(uint32_t hi, uint32_t lo) {
 }
 // Two tagged words (high payload half at the lower address) as one 64-bit
 // device-scope store.
-__device__ __forceinline__ void publish_pair(uint32_t* p, uint32_t bits, uint32_t tag) {
+__device__ __forceinline__ void publish_pair(uint32_t* p, uint32_t bits, uint32_t tag,
+                                             bool xcd = false) {
     const uint64_t w = ((uint64_t)(tag | (bits & 0xffffu)) << 32) | (tag | (bits >> 16));
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    if (xcd)
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void publish_f32(uint32_t* p, float f, uint32_t tag) {
-    publish_pair(p, __float_as_uint(f), tag);
+__device__ __forceinline__ void publish_f32(uint32_t* p, float f, uint32_t tag, bool xcd = false) {
+    publish_pair(p, __float_as_uint(f), tag, xcd);
 }
-__device__ __forceinline__ void publish_f64(uint32_t* p, double d, uint32_t tag) {
+__device__ __forceinline__ void publish_f64(uint32_t* p, double d, uint32_t tag, bool xcd = false) {
     const uint64_t b = (uint64_t)__double_as_longlong(d);
-    publish_pair(p, (uint32_t)(b >> 32), tag);
-    publish_pair(p + 2, (uint32_t)b, tag);
+    publish_pair(p, (uint32_t)(b >> 32), tag, xcd);
+    publish_pair(p + 2, (uint32_t)b, tag, xcd);
+}
+__device__ __forceinline__ void st_xcd(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // ---------------------------------------------------------------- the layer kernel
@@ -498,8 +517,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         return;
     }
     ATTN_TRACE(0);
-    const int h = (wg >> 3) & (kHeads - 1);
-    const int k = (wg & 7) + 8 * (wg >> 7);
+    const int h = (wg & 7) + 8 * ((wg >> 3) & 1);
+    const int k = wg >> 4;
     const int n_pos = pos + 1;
     const int C = (n_pos + kChunks - 1) / kChunks;      // positions per chunk
     const int n_used = (n_pos + C - 1) / C;             // chunks holding positions
@@ -515,8 +534,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     const uint2 gb = P.norm_in ? reinterpret_cast<const uint2*>(P.norm_in)[tid]
                                : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
     const float x_own = tid < kOpRows ? P.x[kOpRows * wg + tid] : 0.f;
-    const int r0 = wg + kWG * wave;                       // < 2048
-    const int r1 = wg + kWG * (wave + kWaves);            // valid below 3648
+    // q rows of head h: 12 per workgroup (i = wave, and wave + 8 for waves
+    // 0..3); kv_a rows: 3072 + wg + 256 i for waves 4..6 (i = wave - 4, the
+    // last only for wg < 64)
+    const int r0 = h * (kNope + kRope) + k + kChunks * wave;
+    const int r1 = wave < 4 ? h * (kNope + kRope) + k + kChunks * (wave + kWaves)
+                 : wave < 7 ? kQDim + wg + kWG * (wave - 4) : kQkvRows;
     u32x4 wq0[4], wq1[4];
     load_row(P.qkv, r0, wq0);
     if (r1 < kQkvRows) {
@@ -537,11 +560,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         float a0, a1;
         dot_rows2_bf16(wq0, wq1, two, xq, xnorm, a0, a1);
         if (lane == 0) {
+            // q words stay on this XCD (head h's workgroups); kv_a is device-wide
             ws->qkv[r0] = a0;
-            st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
+            st_xcd(&ws->qkv_t[r0], tag | bf16_bits(a0));
             if (two) {
                 ws->qkv[r1] = a1;
-                st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
+                if (wave < 4) st_xcd(&ws->qkv_t[r1], tag | bf16_bits(a1));
+                else st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
             }
         }
     }
@@ -623,7 +648,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             for (int p = 0; p < kUkRows; ++p) s += L.u.s2.uk2[p][tid];
             const float qc = (float)s;
             ws->qc[h][kQcCols * k + tid] = qc;
-            publish_f32(ws->qc_t[h][kQcCols * k + tid], qc, tag);
+            publish_f32(ws->qc_t[h][kQcCols * k + tid], qc, tag, true);
         }
         __syncthreads();
     }
@@ -784,10 +809,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             O = fma(L.u.s3.wf[w], L.u.s3.wo[w][tid], O);
             Ls = fma(L.u.s3.wf[w], L.u.s3.wl[w], Ls);
         }
-        publish_f64(ws->o_t[h][k][tid], O, tag);
+        publish_f64(ws->o_t[h][k][tid], O, tag, true);
         if (tid == 0) {
-            publish_f64(&ws->ml_t[h][k][0], M, tag);
-            publish_f64(&ws->ml_t[h][k][4], Ls, tag);
+            publish_f64(&ws->ml_t[h][k][0], M, tag, true);
+            publish_f64(&ws->ml_t[h][k][4], Ls, tag, true);
         }
     }
     ATTN_TRACE(9);
@@ -822,7 +847,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
                 O = fma(L.u.s4.f[q], L.u.s4.mo[q][tid], O);
                 Ls = fma(L.u.s4.f[q], L.u.s4.ml[q], Ls);
             }
-            publish_f32(ws->oc_t[h][kQcCols * k + tid], (float)(O / Ls), tag);
+            publish_f32(ws->oc_t[h][kQcCols * k + tid], (float)(O / Ls), tag, true);
         }
         ATTN_TRACE(11);
         // o_c of head h, columns 64 wave .. 64 wave + 63 (two per lane)
