@@ -675,6 +675,231 @@ __device__ void d_item_m(const Params& P, const Lds& L, const Unit& u, int rb, i
     }
 }
 
+// ---------------------------------------------------------------- MFMA stream
+// The MFMA items of a phase with the token operand held in registers. Wave w
+// takes token tile tt = w % 4 (16 tokens of the pass) and the 256-K slices of
+// parity kh = w / 4; it loads that operand once per (unit, pass): 16-byte
+// fragments of its tokens' x (or h) rows, one per 32-K MFMA step. The weight
+// rows (32 per item) stream through a ring of kRing 16 KB LDS slices, filled
+// by every wave with 1 KB global_load_lds copies (XOR-swizzled as in
+// m_setup) and kept kRing slices ahead across item boundaries, so an item
+// boundary costs no pipeline restart. Each barrier covers two slices, one per
+// parity, computed side by side; an item's two K halves are added (even half
+// + odd half) by the even-parity waves after the next barrier, the odd half
+// crossing in LDS. Every weight byte is read once and each token row once
+// per (workgroup, unit, pass), where the LDS token operand of m_run reads it
+// once per item.
+constexpr int kRing = 8;
+constexpr int kBMax = 32;                      // fragments per wave: G 32, routed D 24
+static_assert(kRing * kSliceA + 4 * kLanes * 8 * 4 <= kNBuf * kSliceBytes, "ring fits mbuf");
+
+struct MRef {
+    int unit, rb, pass;
+};
+
+// n-th MFMA item of the phase in this workgroup's segments (phase D: routed
+// units only; the shared down rows, K = 2816, go through m_run).
+template <bool kG>
+__device__ __forceinline__ bool m_item_n(const Lds& L, int n, MRef& r) {
+    const Seg* S = kG ? L.gseg : L.dseg;
+    const int ns = kG ? L.n_gseg : L.n_dseg;
+    for (int s = 0; s < ns; ++s) {
+        const Unit& u = L.unit[S[s].unit];
+        if (is_v(u.m) || (!kG && u.expert < 0)) continue;
+        const int cnt = S[s].hi - S[s].lo;
+        if (n < cnt) {
+            const int pr = passes_of(u.m);
+            const int i = S[s].lo + n;
+            r.unit = S[s].unit;
+            r.rb = i / pr;
+            r.pass = i - r.rb * pr;
+            return true;
+        }
+        n -= cnt;
+    }
+    return false;
+}
+
+template <bool kG>
+__device__ __forceinline__ const uint16_t* m_weights(const Params& P, const Unit& u) {
+    if (kG) return u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
+    return P.experts + (int64_t)u.expert * P.expert_stride + (int64_t)2 * kInter * kHidden;
+}
+
+// s_waitcnt vmcnt(n), n wave-uniform in [0, 2 kRing].
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+        case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+        case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+        case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+        case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+        case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+        case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+        case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+        case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+        case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+        case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F7F); break;   // 15
+    }
+}
+
+template <bool kG>
+__device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
+    constexpr int K = kG ? kHidden : kInter;            // 2048 / 1408
+    constexpr int S = kG ? 8 : 6;                       // slices per item (D: 5 and a half)
+    constexpr int KS = kG ? 32 : 24;                    // fragments per wave
+    static_assert(KS <= kBMax && S % 2 == 0 && 2 * kRing <= 16, "stream shape");
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int tt = wave & 3, kh = wave >> 2;
+    int n_items = 0;
+    {
+        MRef r;
+        while (m_item_n<kG>(L, n_items, r)) ++n_items;
+    }
+    if (n_items == 0) return;
+    const int total = n_items * S;
+    uint8_t* ring = L.mbuf[0];
+    float* xch = reinterpret_cast<float*>(ring + kRing * kSliceA);   // [4 waves][8][64]
+
+    // this wave's two 1 KB copies of a slice: rows 4 wave + 2 c + lane / 32;
+    // the item's row base is looked up once per item (the copies of one item
+    // are issued in order)
+    int is_item = -1;
+    const uint8_t* is_rows = nullptr;
+    auto issue = [&](int g) {
+        const int item = g / S, s = g - item * S;
+        if (item != is_item) {
+            MRef r;
+            m_item_n<kG>(L, item, r);
+            const uint16_t* A = m_weights<kG>(P, L.unit[r.unit]);
+            is_rows = reinterpret_cast<const uint8_t*>(A + (int64_t)kMRows * r.rb * K);
+            is_item = item;
+        }
+        const bool half = !kG && s == S - 1;
+        uint8_t* dst = ring + (g % kRing) * kSliceA;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int row = 4 * wave + 2 * c + (lane >> 5);
+            const int key = row & 15, p = lane & 31;
+            const uint8_t* src = is_rows + (int64_t)row * K * 2 + kRowSlice * s;
+            const int chunk = half ? ((p & 15) ^ key) : (p ^ key);
+            __builtin_amdgcn_global_load_lds(src + chunk * 16, dst + (4 * wave + 2 * c) * kRowSlice,
+                                             16, 0, 0);
+        }
+    };
+
+    u32x4 bf[KS];
+    MRef cur{-1, -1, -1}, done{-1, -1, -1};
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    bool live = false;
+
+    // even-parity waves: the finished item's total and its outputs
+    auto epilogue = [&](const MRef& r) {
+        const Unit& u = L.unit[r.unit];
+        const int j0 = kMGroup * r.pass;
+        const int m = min(kMGroup, u.m - j0);
+        const int q = lane >> 4, j = lane & 15, jj = 16 * tt + j;
+        if (jj >= m) return;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const float* o = xch + ((tt * 2 + rt) * 4) * kLanes + lane;
+            const float t0 = acc[rt][0] + o[0], t1 = acc[rt][1] + o[kLanes];
+            const float t2 = acc[rt][2] + o[2 * kLanes], t3 = acc[rt][3] + o[3 * kLanes];
+            if (kG) {
+                const float h0 = bf16r(bf16r(silu_rn(bf16r(t0))) * bf16r(t1));
+                const float h1 = bf16r(bf16r(silu_rn(bf16r(t2))) * bf16r(t3));
+                P.hp[u.h_off + (int64_t)(j0 + jj) * (gpairs_of(u) / 2) + 8 * r.rb + 4 * rt + q] =
+                    pack_bf16(h0, h1);
+            } else {
+                const int w0 = 16 * r.rb + 8 * rt + 2 * q;
+                put_part(P, L, u, j0 + jj, w0, t0, t1, epoch);
+                put_part(P, L, u, j0 + jj, w0 + 1, t2, t3, epoch);
+            }
+        }
+    };
+
+    int issued = 0;
+    for (int item = 0; item < n_items; ++item) {
+        MRef r;
+        m_item_n<kG>(L, item, r);
+        if (r.unit != cur.unit || r.pass != cur.pass) {
+            // new token operand: everything in flight lands first, so the
+            // slice waits below stay exact
+            wait_vm(0);
+            const Unit& u = L.unit[r.unit];
+            const int j0 = kMGroup * r.pass;
+            const int m = min(kMGroup, u.m - j0);
+            live = 16 * tt < m;
+            const int t = 16 * tt + (lane & 15);
+            const uint16_t* row;
+            if (kG) row = P.x + (int64_t)token_of(L, u, j0 + (t < m ? t : 0)) * kHidden;
+            else row = reinterpret_cast<const uint16_t*>(P.hp + u.h_off) +
+                       (int64_t)(j0 + (t < m ? t : 0)) * K;
+#pragma unroll
+            for (int f = 0; f < KS; ++f) {
+                const int sl = kh + 2 * (f >> 3), ks = f & 7;
+                const int e = kKs * sl + 32 * ks + 8 * (lane >> 4);
+                bf[f] = e < K ? *reinterpret_cast<const u32x4*>(row + e) : u32x4{0u, 0u, 0u, 0u};
+            }
+            // the operand is complete from here on (an explicit wait the
+            // compiler accounts for, so it adds none before the MFMAs, where
+            // slice copies of unknown count are in flight)
+            wait_vm(0);
+            cur = r;
+        }
+        if (item == 0)   // the ring fills behind the first operand, not before it
+            for (; issued < total && issued < kRing; ++issued) issue(issued);
+        // step j: slices 2j (even-parity waves) and 2j + 1 (odd) of the item
+#pragma unroll
+        for (int j = 0; j < S / 2; ++j) {
+            const int g0 = item * S + 2 * j;
+            // this wave's copies of both slices have landed when at most the
+            // later slices' copies are outstanding (copies complete in order)
+            wait_vm(2 * (issued - g0 - 2));
+            lds_barrier();
+            if (j == 0 && item > 0 && kh == 0) epilogue(done);
+            // the slots of the previous step are free: keep the ring full
+            while (issued < total && issued < g0 + kRing) issue(issued++);
+            if (j == 0) acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (live) {
+                const uint8_t* base = ring + ((g0 + kh) % kRing) * kSliceA;
+                const int rr = lane & 15, kq = lane >> 4;
+                const int nks = (!kG && j == S / 2 - 1 && kh == 1) ? 4 : 8;   // the half slice
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    u32x4 a[8];
+#pragma unroll
+                    for (int ks = 0; ks < 8; ++ks)
+                        a[ks] = *reinterpret_cast<const u32x4*>(
+                            base + (16 * rt + rr) * kRowSlice + (((4 * ks + kq) ^ rr) * 16));
+#pragma unroll
+                    for (int ks = 0; ks < 8; ++ks)
+                        if (ks < nks) acc[rt] = mfma16(a[ks], bf[8 * j + ks], acc[rt]);
+                }
+            }
+            if (j == S / 2 - 1) {
+                if (kh == 1) {
+                    float* o = xch + ((tt * 2) * 4) * kLanes + lane;
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[(rt * 4 + i) * kLanes] = acc[rt][i];
+                }
+                done = r;
+            }
+        }
+    }
+    lds_barrier();
+    if (kh == 0) epilogue(done);
+    __syncthreads();    // the ring and the staging area are reused afterwards
+}
+
 // h rows of a VALU unit (plain words, written by the previous launch) into
 // LDS as bf16 [m][I].
 __device__ void stage_h_plain(const Params& P, const Unit& u, uint8_t* stage) {
@@ -767,19 +992,21 @@ __device__ void v_items(const Params& P, Lds& L, uint32_t epoch) {
     }
 }
 
-// MFMA items of a phase, taken by the whole workgroup in order.
+// MFMA items of a phase, taken by the whole workgroup in order: the gate/up
+// and routed down items through m_stream, the shared down items (K = 2816)
+// one at a time through m_run.
 template <bool kG>
 __device__ void m_items(const Params& P, Lds& L, uint32_t epoch) {
-    const Seg* S = kG ? L.gseg : L.dseg;
-    const int ns = kG ? L.n_gseg : L.n_dseg;
-    for (int s = 0; s < ns; ++s) {
+    if (kG) {
+        m_stream<true>(P, L, epoch);
+        return;
+    }
+    const Seg* S = L.dseg;
+    for (int s = 0; s < L.n_dseg; ++s) {
         const Unit& u = L.unit[S[s].unit];
         if (is_v(u.m)) continue;
         const int pr = passes_of(u.m);
-        for (int i = S[s].lo; i < S[s].hi; ++i) {
-            if (kG) g_item_m(P, L, u, i / pr, i % pr);
-            else d_item_m(P, L, u, i / pr, i % pr, epoch);
-        }
+        for (int i = S[s].lo; i < S[s].hi; ++i) d_item_m(P, L, u, i / pr, i % pr, epoch);
     }
 }
 

@@ -59,6 +59,27 @@ def test_grouped_matches_oracle(dev, T):
     assert runner.status() == 0
 
 
+@pytest.mark.parametrize("T", [8, 9, 256])
+def test_grouped_edges_uniform_routing(dev, T):
+    """Unbiased routing at the edges of the launch plans: T = 8 (the largest
+    single-launch step), T = 9 (the smallest two-launch step, the first with
+    MFMA-eligible units) and T = 256 (the largest step: every expert an MFMA
+    unit, the shared expert four 64-token passes)."""
+    layer, pl = dev
+    runner = ops.GroupedRunner(T, DSV2_LITE)
+    xn = orc.rms_norm(synth.hidden_inputs(50 + T, T))
+    _, ids, ws = orc.route(pl.router_f32(), xn)
+    say(f"grouped edge T={T} distinct={len(np.unique(ids))}")
+    out = runner.run(layer, torch.from_numpy(orc.bf16_bits(xn).view(np.int16)).cuda(),
+                     torch.from_numpy(ids).cuda(), torch.from_numpy(ws).cuda())
+    torch.cuda.synchronize()
+    got = ops.bf16_bits_to_f32(out).cpu().numpy()
+    want = orc.moe_grouped(pl, xn, ids, ws)["out"]
+    assert rel_err(got, want) <= 1e-2
+    assert np.mean(got == want) > 0.95
+    assert runner.status() == 0
+
+
 def test_grouped_equals_batch1_decode(dev):
     """grouped(T) == T batch-1 MoE outputs (decode kernel's moe_out)."""
     layer, pl = dev
