@@ -17,11 +17,14 @@
 //     held in LDS (dot2, one multi-value wave reduction per item), one item
 //     per wave from an LDS ticket.
 //   * MFMA units (> 8 tokens): items of 32 rows x up to 64 tokens taken by
-//     the whole workgroup: 128-element K slices of the weight rows and of the
-//     token rows go straight to LDS (global_load_lds, 1 KB per instruction,
-//     XOR-swizzled so the MFMA operand reads are conflict-free), three slices
-//     in flight, one barrier per slice; wave w runs bf16 MFMA 16x16x32 for
-//     row tile w / 4 and token tile w % 4.
+//     the whole workgroup, bf16 MFMA 16x16x32. Gate/up items stream
+//     (m_stream): each wave keeps its 16 tokens' x fragments for one K parity
+//     in registers, and the weight rows pass through a ring of 256-element K
+//     slices in LDS (global_load_lds, 1 KB per instruction, XOR-swizzled so
+//     the MFMA operand reads are conflict-free) kept 8 slices ahead across
+//     items. Down items (m_run) copy both the weight rows and the token rows
+//     of each slice to LDS, two slices in flight, one barrier per slice; wave
+//     w takes row tile w / 4 and token tile w % 4.
 // T <= 8 (every unit is a VALU unit): ONE launch, phases G (gate/up + SwiGLU)
 //   -> D (down) -> C (combine) handing data over through self-validating words
 //   (epoch << 32 | payload, device-scope stores and loads; no grid barrier).
