@@ -36,11 +36,11 @@
 //   S5 oproj  workgroup w: rows 8w .. 8w+7 of o_proj, bf16, residual add.
 // Workgroup w has (h, k) = (w % 8 + 8 ((w / 8) % 2), w / 16): workgroups are
 // dealt to the 8 XCDs round-robin (w % 8), so all 16 workgroups of a head
-// share one XCD and its L2. Everything that passes between the workgroups of
-// one head (its q rows, q_c, the chunk partials, o_c) is stored into that L2
-// only (workgroup-scope stores) and found there by the device-scope polls;
-// only kv_a (every head needs the new cache row) and the head outputs
-// (o_proj needs all of them) are written through to memory.
+// share one XCD, and what passes between them (its q rows, q_c, the chunk
+// partials, o_c) is written and polled through that XCD's L2: a
+// device-scope poll on the producer's XCD sees the word sooner than one on
+// another XCD. Every word is published with a device-scope store, so the
+// protocol does not depend on that placement, only its speed does.
 // The position can come from the host (an argument) or from device memory
 // (pos_dev), so a whole decode step can be captured once in a HIP graph and
 // replayed: the argmax kernel then advances *pos_dev itself. A device
@@ -382,11 +382,7 @@ __device__ __forceinline__ bool tagged(const u32x4& v, uint32_t tag) {
 // runs out (or finds the sticky status set by another wait) raises
 // FLEET_MOE_ABORT_ATTN_WAIT and returns false; the caller carries on with
 // whatever was read, so the grid always drains.
-// Polls are device-scope loads, which are served by the XCD's own L2 when
-// it holds the line. XCD-local words (producer and consumer on one XCD) are
-// stored at workgroup scope: the store stops in that L2 instead of writing
-// through to memory, and a consumer on the same XCD sees it about half a
-// round trip sooner (a consumer on another XCD would not see it at all).
+
 __device__ bool poll16(const void* base, int off, bool active, uint32_t tag, u32x4& v,
                        Workspace* ws) {
     const __amdgpu_buffer_rsrc_t r = rsrc(base);
@@ -420,26 +416,18 @@ __device__ __forceinline__ float tagged_f32(uint32_t hi, uint32_t lo) {
 }
 // Two tagged words (high payload half at the lower address) as one 64-bit
 // device-scope store.
-__device__ __forceinline__ void publish_pair(uint32_t* p, uint32_t bits, uint32_t tag,
-                                             bool xcd = false) {
+__device__ __forceinline__ void publish_pair(uint32_t* p, uint32_t bits, uint32_t tag) {
     const uint64_t w = ((uint64_t)(tag | (bits & 0xffffu)) << 32) | (tag | (bits >> 16));
-    if (xcd)
-        __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_WORKGROUP);
-    else
-        __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void publish_f32(uint32_t* p, float f, uint32_t tag, bool xcd = false) {
-    publish_pair(p, __float_as_uint(f), tag, xcd);
+__device__ __forceinline__ void publish_f32(uint32_t* p, float f, uint32_t tag) {
+    publish_pair(p, __float_as_uint(f), tag);
 }
-__device__ __forceinline__ void publish_f64(uint32_t* p, double d, uint32_t tag, bool xcd = false) {
+__device__ __forceinline__ void publish_f64(uint32_t* p, double d, uint32_t tag) {
     const uint64_t b = (uint64_t)__double_as_longlong(d);
-    publish_pair(p, (uint32_t)(b >> 32), tag, xcd);
-    publish_pair(p + 2, (uint32_t)b, tag, xcd);
-}
-__device__ __forceinline__ void st_xcd(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    publish_pair(p, (uint32_t)(b >> 32), tag);
+    publish_pair(p + 2, (uint32_t)b, tag);
 }
 
 // ---------------------------------------------------------------- the layer kernel
@@ -560,13 +548,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         float a0, a1;
         dot_rows2_bf16(wq0, wq1, two, xq, xnorm, a0, a1);
         if (lane == 0) {
-            // q words stay on this XCD (head h's workgroups); kv_a is device-wide
             ws->qkv[r0] = a0;
-            st_xcd(&ws->qkv_t[r0], tag | bf16_bits(a0));
+            st_agent(&ws->qkv_t[r0], tag | bf16_bits(a0));
             if (two) {
                 ws->qkv[r1] = a1;
-                if (wave < 4) st_xcd(&ws->qkv_t[r1], tag | bf16_bits(a1));
-                else st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
+                st_agent(&ws->qkv_t[r1], tag | bf16_bits(a1));
             }
         }
     }
@@ -648,7 +634,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             for (int p = 0; p < kUkRows; ++p) s += L.u.s2.uk2[p][tid];
             const float qc = (float)s;
             ws->qc[h][kQcCols * k + tid] = qc;
-            publish_f32(ws->qc_t[h][kQcCols * k + tid], qc, tag, true);
+            publish_f32(ws->qc_t[h][kQcCols * k + tid], qc, tag);
         }
         __syncthreads();
     }
@@ -809,10 +795,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             O = fma(L.u.s3.wf[w], L.u.s3.wo[w][tid], O);
             Ls = fma(L.u.s3.wf[w], L.u.s3.wl[w], Ls);
         }
-        publish_f64(ws->o_t[h][k][tid], O, tag, true);
+        publish_f64(ws->o_t[h][k][tid], O, tag);
         if (tid == 0) {
-            publish_f64(&ws->ml_t[h][k][0], M, tag, true);
-            publish_f64(&ws->ml_t[h][k][4], Ls, tag, true);
+            publish_f64(&ws->ml_t[h][k][0], M, tag);
+            publish_f64(&ws->ml_t[h][k][4], Ls, tag);
         }
     }
     ATTN_TRACE(9);
@@ -847,7 +833,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
                 O = fma(L.u.s4.f[q], L.u.s4.mo[q][tid], O);
                 Ls = fma(L.u.s4.f[q], L.u.s4.ml[q], Ls);
             }
-            publish_f32(ws->oc_t[h][kQcCols * k + tid], (float)(O / Ls), tag, true);
+            publish_f32(ws->oc_t[h][kQcCols * k + tid], (float)(O / Ls), tag);
         }
         ATTN_TRACE(11);
         // o_c of head h, columns 64 wave .. 64 wave + 63 (two per lane)
