@@ -170,24 +170,6 @@ __device__ __forceinline__ float dot_row(const u32x4 (&w)[4], const u32x4 (&xq)[
     return (float)wave_sum64(a);
 }
 
-// bf16 of the exactly rounded dot of a K = 2048 bf16 row with a bf16 vector
-// of 2-norm xnorm: the fp32 evaluation (v_dot2 chains of depth 8, a two-level
-// tree, the wave sum: 16 roundings) when certify_bf16 proves its bf16
-// rounding, dot_row otherwise.
-__device__ __forceinline__ float dot_row_bf16(const u32x4 (&w)[4], const u32x4 (&xq)[4],
-                                              float xnorm) {
-    float a[4], n[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        a[m] = dot8_d2(w[m], xq[m], 0.f);
-        n[m] = dot8_d2(w[m], w[m], 0.f);
-    }
-    float r;
-    if (!certify_bf16(wave_sum(tree_sum(a)), wave_sum(tree_sum(n)), xnorm, cert_gamma(16), r))
-        r = bf16r(dot_row(w, xq));
-    return r;
-}
-
 // Two rows at once (the second only if `two`): their dots and sums of
 // squares reduced together (lane % 4: a0, a1, n0, n1), lanes 0 and 1
 // certify, a row the bound cannot decide is evaluated exactly. r0 / r1

@@ -50,19 +50,6 @@ __device__ __forceinline__ uint32_t bf16_bits(float f) {
 }
 __device__ __forceinline__ float bf16r(float f) { return __uint_as_float(bf16_bits(f) << 16); }
 
-// 8-element dot of one 16-byte bf16 chunk with 8 fp32 values, fp32 FMA chain.
-__device__ __forceinline__ float dot8(const u32x4& w, const float* x, float acc) {
-    acc = fmaf(bf_lo(w.x), x[0], acc);
-    acc = fmaf(bf_hi(w.x), x[1], acc);
-    acc = fmaf(bf_lo(w.y), x[2], acc);
-    acc = fmaf(bf_hi(w.y), x[3], acc);
-    acc = fmaf(bf_lo(w.z), x[4], acc);
-    acc = fmaf(bf_hi(w.z), x[5], acc);
-    acc = fmaf(bf_lo(w.w), x[6], acc);
-    acc = fmaf(bf_hi(w.w), x[7], acc);
-    return acc;
-}
-
 // bf16 pair dot with fp32 accumulation (v_dot2c_f32_bf16):
 // acc + a.lo * b.lo + a.hi * b.hi. The products of two bf16 values are exact.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -162,19 +149,6 @@ __device__ __forceinline__ float tree_sum(const float (&v)[N]) {
 }
 constexpr int tree_depth(int n) { return n <= 1 ? 0 : 1 + tree_depth((n + 1) / 2); }
 
-// Same, both operands bf16 chunks.
-__device__ __forceinline__ float dot8_bb(const u32x4& w, const u32x4& h, float acc) {
-    acc = fmaf(bf_lo(w.x), bf_lo(h.x), acc);
-    acc = fmaf(bf_hi(w.x), bf_hi(h.x), acc);
-    acc = fmaf(bf_lo(w.y), bf_lo(h.y), acc);
-    acc = fmaf(bf_hi(w.y), bf_hi(h.y), acc);
-    acc = fmaf(bf_lo(w.z), bf_lo(h.z), acc);
-    acc = fmaf(bf_hi(w.z), bf_hi(h.z), acc);
-    acc = fmaf(bf_lo(w.w), bf_lo(h.w), acc);
-    acc = fmaf(bf_hi(w.w), bf_hi(h.w), acc);
-    return acc;
-}
-
 // Wave reductions with DPP row operations (a few cycles each, no LDS
 // round trip): xor-1 and xor-2 quad permutes, the half-row and row mirrors
 // leave every lane of a 16-lane row holding the row sum, and the four row
@@ -266,15 +240,6 @@ __device__ __forceinline__ double wave_sum64(double v) {
     v += dpp64<0x141>(v);
     v += dpp64<0x140>(v);
     return (readlane64(v, 0) + readlane64(v, 16)) + (readlane64(v, 32) + readlane64(v, 48));
-}
-
-__device__ __forceinline__ int wave_max_i(int v) {
-    v = max(v, FLEET_DPP(v, 0xB1));
-    v = max(v, FLEET_DPP(v, 0x4E));
-    v = max(v, FLEET_DPP(v, 0x141));
-    v = max(v, FLEET_DPP(v, 0x140));
-    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
 // Value of lane 0 in every lane (all lanes must be active).
