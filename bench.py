@@ -122,9 +122,7 @@ def main() -> int:
     blob, lay = synth.moe_layer_blob(seed=0, layer=1, dims=dims)
     layer = ops.DeviceLayer.from_host(blob, lay, 1, dims, device=dev)
     n_tok = max(args.steps, 1)
-    x_host = synth.hidden_inputs(0, max(n_tok, args.warmup))
-    x_host = ((x_host.view(np.uint32) + 0x7FFF + ((x_host.view(np.uint32) >> 16) & 1))
-              & 0xFFFF0000).astype(np.uint32).view(np.float32)       # bf16-valued tokens
+    x_host = bf16_tokens(synth, max(n_tok, args.warmup))
     xd = torch.from_numpy(x_host).to(dev)
     outs = torch.empty_like(xd)
     ids = torch.empty((xd.shape[0], dims.top_k), dtype=torch.int32, device=dev)
@@ -221,7 +219,9 @@ def main() -> int:
     }
 
     if not args.no_grouped:
-        result["grouped"] = bench_grouped(torch, dev, stream, layer, dims, x_host)
+        # the grouped step takes up to 64 tokens whatever --steps is
+        gx = x_host if x_host.shape[0] >= 64 else bf16_tokens(synth, 64)
+        result["grouped"] = bench_grouped(torch, dev, stream, layer, dims, gx)
     if not args.no_column:
         del layer
         torch.cuda.empty_cache()
@@ -404,6 +404,14 @@ def stream_ceiling(torch, dev, stream, lib):
             "kernel": "fleet_moe::probe::stream_read_kernel"}
 
 
+def bf16_tokens(synth, n):
+    """The first n seeded N(0,1) hidden vectors (a prefix-stable stream),
+    rounded to bf16 (RNE), as fp32."""
+    x = synth.hidden_inputs(0, n)
+    return ((x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1))
+            & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
 def bench_grouped(torch, dev, stream, layer, dims, x_host):
     """Config 2: T in {4, 16, 64}, Zipf(1.1)-biased routing; times the grouped
     product alone (routing precomputed), per step."""
@@ -412,6 +420,8 @@ def bench_grouped(torch, dev, stream, layer, dims, x_host):
     bias = torch.from_numpy(synth.zipf_logit_bias(0)).to(dev)
     runner = ops.GroupedRunner(64, dims, device=dev)
     for T in (4, 16, 64):
+        if x_host.shape[0] < T:
+            raise ValueError(f"grouped step T={T} needs {T} token rows, got {x_host.shape[0]}")
         x = torch.from_numpy(x_host[:T]).to(dev)
         # the router kernel takes normed input: the RMSNorm of config 2 (unit
         # gamma) is applied with torch here, outside the timed expert product

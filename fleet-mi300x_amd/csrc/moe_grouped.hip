@@ -64,17 +64,14 @@ constexpr int kStageBytes = 3 * kVMax * kInter * 2;   // 67,584
 static_assert(2 * kVMax * kHidden * 2 <= kStageBytes, "x staging fits");
 static_assert(kVMax * (kSharedInter + kInter) * 2 <= kStageBytes, "h staging fits");
 
-// MFMA items: 32 rows x 64 tokens, K in slices of 256 (512 B of every row)
-// through LDS; a K of 1408 ends with a half slice.
+// MFMA items: 32 weight rows x up to 64 tokens; the rows pass through LDS in
+// K slices of 256 (512 B of every row; a K of 1408 ends with a half slice).
 constexpr int kMRows = 32;
 constexpr int kKs = 256;
 constexpr int kRowSlice = kKs * 2;                 // 512 B
 constexpr int kSliceA = kMRows * kRowSlice;        // 16 KB
-constexpr int kSliceB = kMGroup * kRowSlice;       // 32 KB
-constexpr int kSliceBytes = kSliceA + kSliceB;     // 48 KB
-constexpr int kNBuf = 3;                           // two slices in flight
-constexpr int kLoadsPerWave = kSliceBytes / 1024 / kWaves;   // 6 x 1 KB per wave per slice
-static_assert(kSliceBytes % (1024 * kWaves) == 0, "slice loads split over the waves");
+constexpr int kRing = 8;                           // slices in flight
+constexpr int kXchBytes = 4 * 8 * kLanes * 4;      // odd-K-half partials, 8 KB
 
 // Sticky status bit beside FLEET_MOE_ABORT_*: LDS staging overflow (the
 // partition bounds make it unreachable; checked anyway).
@@ -90,7 +87,7 @@ struct Header {
 static_assert(offsetof(Header, abort) == 8, "status word offset");
 
 struct Layout {
-    size_t h, hp, part, total;
+    size_t h, hp, part, sp, total;
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -100,7 +97,8 @@ __host__ __device__ inline Layout layout(int max_tokens) {
     L.h = align256(sizeof(Header));
     L.hp = L.h + align256((size_t)(max_tokens < kVMax ? max_tokens : kVMax) * kHWordsPerToken * 8);
     L.part = L.hp + align256((size_t)max_tokens * kHWordsPerToken * 4);
-    L.total = L.part + align256((size_t)max_tokens * kSlots * kPartWords * 8);
+    L.sp = L.part + align256((size_t)max_tokens * kSlots * kPartWords * 8);
+    L.total = L.sp + align256((size_t)max_tokens * 2 * kHidden * 8);
     return L;
 }
 
@@ -116,6 +114,7 @@ struct Params {
     uint64_t* h;               // tagged h words (single launch)
     uint32_t* hp;              // plain h words, two bf16 each (two launches)
     uint64_t* part;            // tagged partial words [T][7][1024]
+    uint64_t* sp;              // tagged fp32 shared down sums [T][2 K halves][2048] (two launches)
     int T;
 };
 
@@ -146,7 +145,7 @@ struct Lds {
     float red[kWaves][kLanes];
     union {
         alignas(16) uint8_t stage[kStageBytes];          // VALU units: x or h rows
-        alignas(16) uint8_t mbuf[kNBuf][kSliceBytes];    // MFMA items: K slices
+        alignas(16) uint8_t ring[kRing * kSliceA + kXchBytes];   // MFMA items
         struct {                                         // prologue only
             int8_t id[kMaxEntries];      // ids, clamped to [0, 64)
             int16_t rank[kMaxEntries];   // rank of an entry among equal ids of its chunk
@@ -165,7 +164,8 @@ __device__ __forceinline__ int d_rows_v(const Unit& u) {
 }
 
 // Items and their cost (G: 16 KB units; D: 11 KB units) of a unit. MFMA items
-// run pass-minor: item i is row block i / passes, token pass i % passes.
+// run pass-minor: item i is row block i / passes, token pass i % passes; the
+// shared expert's MFMA down items are two K halves of that sequence.
 __device__ __forceinline__ void g_items_of(const Unit& u, int& n, int& cost) {
     const int pairs = gpairs_of(u);
     if (is_v(u.m)) { n = pairs / 2; cost = 1; }
@@ -178,8 +178,8 @@ __device__ __forceinline__ void d_items_of(const Unit& u, int& n, int& cost) {
         n = kHidden / R;
         cost = sh ? R / 2 : R / 4;
     } else {
-        n = kHidden / kMRows * passes_of(u.m);
-        cost = sh ? 16 : 8;
+        n = (sh ? 2 : 1) * (kHidden / kMRows) * passes_of(u.m);
+        cost = 8;
     }
 }
 
@@ -426,149 +426,6 @@ __device__ __forceinline__ void g_item_v(const Params& P, Lds& L, const Unit& u,
     lds_wave_sync();
 }
 
-// ---------------------------------------------------------------- MFMA items
-
-// One workgroup-cooperative MFMA item: rows [r0, r0 + 32) of A (bf16, row
-// stride lda elements) times the rows of up to 64 tokens, K = 256 S (+ 128 for
-// a half tail slice), through LDS. Slice s: A row r at [r * 512 B), token row
-// t at 16 KB + [t * 512 B); the 16-byte chunk c of row x sits in slot
-// c ^ (x & 15), so the 16 rows an MFMA operand read touches hit 16 different
-// slots (all 64 banks once). A slice takes 16 + 8 nt 1 KB loads (nt live
-// token tiles): load n < 16 covers A rows 2n, 2n + 1, load n >= 16 token rows
-// 2(n-16), +1; lane l takes row 2n + l / 32, slot l % 32. Wave w issues the
-// contiguous block of loads [w p, w p + p), p = ceil(total / 8) <= 6. Wave w
-// computes row tile w / 4 x token tile w % 4
-// (if live) and returns D[4 (lane / 16) + v][lane % 16].
-struct MItem {
-    const uint8_t* gsrc[kLoadsPerWave];   // this lane's global source, full slices
-    const uint8_t* gtail[kLoadsPerWave];  // same for a half slice (chunks 0..15 only)
-    int ldst[kLoadsPerWave];              // LDS offset of each of this wave's loads
-    int mine;                             // loads this wave issues per slice
-};
-
-__device__ __forceinline__ void m_issue(Lds& L, const MItem& it, int s, int buf, bool tail) {
-#pragma unroll
-    for (int n = 0; n < kLoadsPerWave; ++n)
-        if (n < it.mine)
-            __builtin_amdgcn_global_load_lds((tail ? it.gtail[n] : it.gsrc[n]) + s * kRowSlice,
-                                             L.mbuf[buf] + it.ldst[n], 16, 0, 0);
-}
-
-// All operands of the slice are read before its MFMAs (the waves run in step
-// between barriers and cannot hide each other's LDS latency).
-template <int Q>
-__device__ __forceinline__ f32x4 m_compute(const Lds& L, int buf, f32x4 acc) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const int r = lane & 15, kq = lane >> 4;
-    const int rt = wave >> 2, tt = wave & 3;
-    const uint8_t* base = L.mbuf[buf];
-    u32x4 a[Q], b[Q];
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-        const int slot = (4 * q + kq) ^ r;
-        a[q] = *reinterpret_cast<const u32x4*>(base + (16 * rt + r) * kRowSlice + slot * 16);
-        b[q] = *reinterpret_cast<const u32x4*>(base + kSliceA + (16 * tt + r) * kRowSlice +
-                                                slot * 16);
-    }
-#pragma unroll
-    for (int q = 0; q < Q; ++q) acc = mfma16(a[q], b[q], acc);
-    return acc;
-}
-
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 6].
-__device__ __forceinline__ void wait_loads_except(int n) {
-    switch (n) {
-        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-        case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-        default: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    }
-}
-
-// S slices (the last one half when `tail`), two in flight: at slice s a wave
-// waits for its own loads of slice s (loads return in order, so "only the next
-// slice's loads outstanding"), the barrier makes every wave's part visible and
-// frees the buffer of slice s - 1, then slice s + 2 is issued into it and
-// slice s computed. The barrier orders LDS only: it does not wait for the
-// loads in flight.
-__device__ f32x4 m_run(Lds& L, const MItem& it, int S, bool tail, bool live) {
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_issue(L, it, 0, 0, tail && S == 1);
-    if (S > 1) m_issue(L, it, 1, 1, tail && S == 2);
-    for (int s = 0; s < S; ++s) {
-        if (s + 1 < S) wait_loads_except(it.mine);   // the next slice's may stay in flight
-        else __builtin_amdgcn_s_waitcnt(0x0F70);     // vmcnt(0)
-        lds_barrier();
-        if (s + 2 < S) m_issue(L, it, s + 2, (s + 2) % kNBuf, tail && s + 3 == S);
-        if (live) {
-            if (tail && s + 1 == S) acc = m_compute<kKs / 64>(L, s % kNBuf, acc);
-            else acc = m_compute<kKs / 32>(L, s % kNBuf, acc);
-        }
-    }
-    __syncthreads();    // the next item reuses the buffers
-    return acc;
-}
-
-// Sources of this wave's loads. A: rows r0.. of `A` (stride lda elements);
-// B: token rows given by `brow(t)` (a pointer to the row's first element).
-template <typename BRow>
-__device__ __forceinline__ MItem m_setup(const uint16_t* A, int64_t lda, int r0, int nt,
-                                         BRow brow) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const int total = kSliceA / 1024 + 8 * nt;
-    const int per = (total + kWaves - 1) / kWaves;
-    MItem it;
-    it.mine = wave_bcast(max(0, min(per, total - wave * per)));   // wave-uniform (SGPR)
-#pragma unroll
-    for (int k = 0; k < kLoadsPerWave; ++k) {
-        const int n = min(wave * per + k, total - 1);   // loads past `mine` are not issued
-        const int p = lane & 31, half = lane >> 5;
-        const uint8_t* row;
-        int key;
-        if (n < kSliceA / 1024) {
-            const int x = 2 * n + half;
-            row = reinterpret_cast<const uint8_t*>(A + (int64_t)(r0 + x) * lda);
-            key = x & 15;
-            it.ldst[k] = n * 1024;
-        } else {
-            const int nb = n - kSliceA / 1024;
-            const int t = 2 * nb + half;
-            row = reinterpret_cast<const uint8_t*>(brow(t));
-            key = t & 15;
-            it.ldst[k] = kSliceA + nb * 1024;
-        }
-        it.gsrc[k] = row + (p ^ key) * 16;
-        it.gtail[k] = row + ((p & 15) ^ key) * 16;
-    }
-    return it;
-}
-
-// MFMA item of phase G: gate/up rows [32 rb, 32 rb + 32) of unit u for its
-// tokens [64 pass, 64 pass + 64); h -> plain words.
-__device__ void g_item_m(const Params& P, Lds& L, const Unit& u, int rb, int pass) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const int j0 = kMGroup * pass;
-    const int m = min(kMGroup, u.m - j0);
-    const uint16_t* W = u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
-    const MItem it = m_setup(W, kHidden, kMRows * rb, (m + 15) >> 4, [&](int t) {
-        return P.x + (int64_t)token_of(L, u, j0 + (t < m ? t : 0)) * kHidden;
-    });
-    const int tt = wave & 3, rt = wave >> 2;
-    const f32x4 acc = m_run(L, it, kHidden / kKs, false, 16 * tt < m);
-    // D rows 4q + v of row tile rt: pair (32 rb + 16 rt + 4q) / 2 + v / 2
-    const int q = lane >> 4, j = lane & 15;
-    const int jj = 16 * tt + j;
-    if (jj < m) {
-        const float h0 = bf16r(bf16r(silu_rn(bf16r(acc[0]))) * bf16r(acc[1]));
-        const float h1 = bf16r(bf16r(silu_rn(bf16r(acc[2]))) * bf16r(acc[3]));
-        P.hp[u.h_off + (int64_t)(j0 + jj) * (gpairs_of(u) / 2) + 8 * rb + 4 * rt + q] =
-            pack_bf16(h0, h1);
-    }
-}
-
 // ---------------------------------------------------------------- phase D
 
 // Partial words of `pos` (unit position) for rows 2w, 2w + 1: routed values
@@ -649,71 +506,51 @@ __device__ __forceinline__ void d_item_v(const Params& P, Lds& L, const Unit& u,
     lds_wave_sync();
 }
 
-// MFMA item of phase D: down rows [32 rb, 32 rb + 32) of unit u for its
-// tokens [64 pass, 64 pass + 64), h from the plain words.
-__device__ void d_item_m(const Params& P, const Lds& L, const Unit& u, int rb, int pass,
-                         uint32_t epoch) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kLanes - 1);
-    const int j0 = kMGroup * pass;
-    const int m = min(kMGroup, u.m - j0);
-    const bool sh = u.expert < 0;
-    const int K = gpairs_of(u);
-    const uint16_t* dn = sh ? P.shared + (int64_t)2 * kSharedInter * kHidden
-                            : P.experts + (int64_t)u.expert * P.expert_stride +
-                                  (int64_t)2 * kInter * kHidden;
-    const uint16_t* hrows = reinterpret_cast<const uint16_t*>(P.hp + u.h_off);
-    const MItem it = m_setup(dn, K, kMRows * rb, (m + 15) >> 4, [&](int t) {
-        return hrows + (int64_t)(j0 + (t < m ? t : 0)) * K;
-    });
-    const int tt = wave & 3, rt = wave >> 2;
-    // K = 1408: five full slices and a half one; K = 2816: eleven full
-    const bool tail = (K % kKs) != 0;
-    const f32x4 acc = m_run(const_cast<Lds&>(L), it, K / kKs + (tail ? 1 : 0), tail, 16 * tt < m);
-    const int q = lane >> 4, j = lane & 15;
-    const int jj = 16 * tt + j;
-    if (jj < m) {
-        const int w0 = 16 * rb + 8 * rt + 2 * q;   // rows 32 rb + 16 rt + 4q .. + 3
-        put_part(P, L, u, j0 + jj, w0, acc[0], acc[1], epoch);
-        put_part(P, L, u, j0 + jj, w0 + 1, acc[2], acc[3], epoch);
-    }
-}
-
 // ---------------------------------------------------------------- MFMA stream
-// The MFMA items of a phase with the token operand held in registers. Wave w
-// takes token tile tt = w % 4 (16 tokens of the pass) and the 256-K slices of
-// parity kh = w / 4; it loads that operand once per (unit, pass): 16-byte
-// fragments of its tokens' x (or h) rows, one per 32-K MFMA step. The weight
-// rows (32 per item) stream through a ring of kRing 16 KB LDS slices, filled
-// by every wave with 1 KB global_load_lds copies (XOR-swizzled as in
-// m_setup) and kept kRing slices ahead across item boundaries, so an item
-// boundary costs no pipeline restart. Each barrier covers two slices, one per
-// parity, computed side by side; an item's two K halves are added (even half
-// + odd half) by the even-parity waves after the next barrier, the odd half
-// crossing in LDS. Every weight byte is read once and each token row once
-// per (workgroup, unit, pass), where the LDS token operand of m_run reads it
-// once per item.
-constexpr int kRing = 8;
-constexpr int kBMax = 32;                      // fragments per wave: G 32, routed D 24
-static_assert(kRing * kSliceA + 4 * kLanes * 8 * 4 <= kNBuf * kSliceBytes, "ring fits mbuf");
+// The MFMA items of a phase, taken by the whole workgroup in order, with the
+// token operand held in registers. Wave w takes token tile tt = w % 4 (16
+// tokens of the pass) and the 256-K slices of parity kh = w / 4; it loads that
+// operand once per (unit, pass, K half): 16-byte fragments of its tokens' x
+// (or h) rows, one per 32-K MFMA step. The weight rows (32 per item) stream
+// through a ring of kRing 16 KB LDS slices, filled by every wave with 1 KB
+// global_load_lds copies and kept kRing slices ahead across item boundaries,
+// so an item boundary costs no pipeline restart. In a slice, row r sits at
+// [r * 512 B) with its 16-byte chunk c in slot c ^ (r & 15), so the 16 rows an
+// MFMA operand read touches hit 16 different slots (all 64 banks once). Each
+// barrier covers two slices, one per parity, computed side by side; an item's
+// two K halves are added (even half + odd half) by the even-parity waves after
+// the next barrier, the odd half crossing in LDS. Every weight byte is read
+// once and each token row once per (workgroup, unit, pass, K half).
+// Phase D: the shared expert's down rows (K = 2816) run as two K halves of
+// 1408, each item shaped like a routed one; their fp32 sums go out as tagged
+// words, and the combine adds the two halves before the bf16 rounding.
+constexpr int kBMax = 32;                      // fragments per wave: G 32, D 24
+static_assert(kSliceA == kWaves * 2 * 1024, "two 1 KB copies per wave per slice");
 
 struct MRef {
-    int unit, rb, pass;
+    int unit, rb, pass, half;
 };
 
-// n-th MFMA item of the phase in this workgroup's segments (phase D: routed
-// units only; the shared down rows, K = 2816, go through m_run).
+// n-th MFMA item of the phase in this workgroup's segments: row block rb,
+// token pass, K half (shared down items only; item i of that unit is half
+// i / (64 passes), then row block and pass as for the others).
 template <bool kG>
 __device__ __forceinline__ bool m_item_n(const Lds& L, int n, MRef& r) {
     const Seg* S = kG ? L.gseg : L.dseg;
     const int ns = kG ? L.n_gseg : L.n_dseg;
     for (int s = 0; s < ns; ++s) {
         const Unit& u = L.unit[S[s].unit];
-        if (is_v(u.m) || (!kG && u.expert < 0)) continue;
+        if (is_v(u.m)) continue;
         const int cnt = S[s].hi - S[s].lo;
         if (n < cnt) {
             const int pr = passes_of(u.m);
-            const int i = S[s].lo + n;
+            int i = S[s].lo + n;
             r.unit = S[s].unit;
+            r.half = 0;
+            if (!kG && u.expert < 0) {
+                r.half = i / ((kHidden / kMRows) * pr);
+                i -= r.half * (kHidden / kMRows) * pr;
+            }
             r.rb = i / pr;
             r.pass = i - r.rb * pr;
             return true;
@@ -723,10 +560,23 @@ __device__ __forceinline__ bool m_item_n(const Lds& L, int n, MRef& r) {
     return false;
 }
 
+// First weight row of item r and the row stride (elements).
 template <bool kG>
-__device__ __forceinline__ const uint16_t* m_weights(const Params& P, const Unit& u) {
-    if (kG) return u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
-    return P.experts + (int64_t)u.expert * P.expert_stride + (int64_t)2 * kInter * kHidden;
+__device__ __forceinline__ const uint16_t* m_rows(const Params& P, const Unit& u, const MRef& r,
+                                                  int& ld) {
+    if (kG) {
+        ld = kHidden;
+        const uint16_t* w = u.expert < 0 ? P.shared : P.experts + (int64_t)u.expert * P.expert_stride;
+        return w + (int64_t)kMRows * r.rb * kHidden;
+    }
+    if (u.expert < 0) {
+        ld = kSharedInter;
+        return P.shared + (int64_t)2 * kSharedInter * kHidden +
+               (int64_t)kMRows * r.rb * kSharedInter + r.half * kInter;
+    }
+    ld = kInter;
+    return P.experts + (int64_t)u.expert * P.expert_stride + (int64_t)2 * kInter * kHidden +
+           (int64_t)kMRows * r.rb * kInter;
 }
 
 // s_waitcnt vmcnt(n), n wave-uniform in [0, 2 kRing].
@@ -753,7 +603,7 @@ __device__ __forceinline__ void wait_vm(int n) {
 
 template <bool kG>
 __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
-    constexpr int K = kG ? kHidden : kInter;            // 2048 / 1408
+    constexpr int K = kG ? kHidden : kInter;            // 2048 / 1408 per item
     constexpr int S = kG ? 8 : 6;                       // slices per item (D: 5 and a half)
     constexpr int KS = kG ? 32 : 24;                    // fragments per wave
     static_assert(KS <= kBMax && S % 2 == 0 && 2 * kRing <= 16, "stream shape");
@@ -767,21 +617,20 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
     }
     if (n_items == 0) return;
     const int total = n_items * S;
-    uint8_t* ring = L.mbuf[0];
+    uint8_t* ring = L.ring;
     float* xch = reinterpret_cast<float*>(ring + kRing * kSliceA);   // [4 waves][8][64]
 
     // this wave's two 1 KB copies of a slice: rows 4 wave + 2 c + lane / 32;
     // the item's row base is looked up once per item (the copies of one item
     // are issued in order)
-    int is_item = -1;
+    int is_item = -1, is_ld = K;
     const uint8_t* is_rows = nullptr;
     auto issue = [&](int g) {
         const int item = g / S, s = g - item * S;
         if (item != is_item) {
             MRef r;
             m_item_n<kG>(L, item, r);
-            const uint16_t* A = m_weights<kG>(P, L.unit[r.unit]);
-            is_rows = reinterpret_cast<const uint8_t*>(A + (int64_t)kMRows * r.rb * K);
+            is_rows = reinterpret_cast<const uint8_t*>(m_rows<kG>(P, L.unit[r.unit], r, is_ld));
             is_item = item;
         }
         const bool half = !kG && s == S - 1;
@@ -790,7 +639,7 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
         for (int c = 0; c < 2; ++c) {
             const int row = 4 * wave + 2 * c + (lane >> 5);
             const int key = row & 15, p = lane & 31;
-            const uint8_t* src = is_rows + (int64_t)row * K * 2 + kRowSlice * s;
+            const uint8_t* src = is_rows + (int64_t)row * is_ld * 2 + kRowSlice * s;
             const int chunk = half ? ((p & 15) ^ key) : (p ^ key);
             __builtin_amdgcn_global_load_lds(src + chunk * 16, dst + (4 * wave + 2 * c) * kRowSlice,
                                              16, 0, 0);
@@ -798,31 +647,55 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
     };
 
     u32x4 bf[KS];
-    MRef cur{-1, -1, -1}, done{-1, -1, -1};
+    MRef cur{-1, -1, -1, -1}, done{-1, -1, -1, -1};
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
     bool live = false;
+    // phase D: where this lane's token of the current (unit, pass, half)
+    // publishes (first word of its routed (token, slot) partial, or of its
+    // shared half's fp32 sums) and its routing weight, set with the operand
+    // so that the epilogue reads no memory but the exchange area (a global
+    // or LDS-table load there would wait for the ring copies in flight); the
+    // dn_ copies belong to the finished item whose epilogue is pending, as
+    // the operand may already be the next unit's
+    bool ep_ok = false, ep_sh = false, dn_ok = false, dn_sh = false;
+    int64_t ep_base = 0, dn_base = 0;
+    float ep_w = 1.f, dn_w = 1.f;
 
     // even-parity waves: the finished item's total and its outputs
     auto epilogue = [&](const MRef& r) {
-        const Unit& u = L.unit[r.unit];
-        const int j0 = kMGroup * r.pass;
-        const int m = min(kMGroup, u.m - j0);
         const int q = lane >> 4, j = lane & 15, jj = 16 * tt + j;
-        if (jj >= m) return;
+        int j0 = 0, m = 0;
+        if (kG) {
+            j0 = kMGroup * r.pass;
+            m = min(kMGroup, L.unit[r.unit].m - j0);
+            if (jj >= m) return;
+        } else if (!dn_ok) {
+            return;
+        }
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             const float* o = xch + ((tt * 2 + rt) * 4) * kLanes + lane;
             const float t0 = acc[rt][0] + o[0], t1 = acc[rt][1] + o[kLanes];
             const float t2 = acc[rt][2] + o[2 * kLanes], t3 = acc[rt][3] + o[3 * kLanes];
             if (kG) {
-                const float h0 = bf16r(bf16r(silu_rn(bf16r(t0))) * bf16r(t1));
-                const float h1 = bf16r(bf16r(silu_rn(bf16r(t2))) * bf16r(t3));
+                const Unit& u = L.unit[r.unit];
                 P.hp[u.h_off + (int64_t)(j0 + jj) * (gpairs_of(u) / 2) + 8 * r.rb + 4 * rt + q] =
-                    pack_bf16(h0, h1);
+                    pack_bf16(bf16r(bf16r(silu_rn(bf16r(t0))) * bf16r(t1)),
+                              bf16r(bf16r(silu_rn(bf16r(t2))) * bf16r(t3)));
+            } else if (dn_sh) {
+                // fp32 sums of rows 32 rb + 16 rt + 4 q + v
+                uint64_t* o2 = P.sp + dn_base + 32 * r.rb + 16 * rt + 4 * q;
+                st_word(o2, epoch, __float_as_uint(t0));
+                st_word(o2 + 1, epoch, __float_as_uint(t1));
+                st_word(o2 + 2, epoch, __float_as_uint(t2));
+                st_word(o2 + 3, epoch, __float_as_uint(t3));
             } else {
+                // words of rows (2 w0, 2 w0 + 1) and (2 w0 + 2, 2 w0 + 3):
+                // bf16(w * bf16(d)), as put_part
                 const int w0 = 16 * r.rb + 8 * rt + 2 * q;
-                put_part(P, L, u, j0 + jj, w0, t0, t1, epoch);
-                put_part(P, L, u, j0 + jj, w0 + 1, t2, t3, epoch);
+                st_word(P.part + dn_base + w0, epoch, pack_bf16(dn_w * bf16r(t0), dn_w * bf16r(t1)));
+                st_word(P.part + dn_base + w0 + 1, epoch,
+                        pack_bf16(dn_w * bf16r(t2), dn_w * bf16r(t3)));
             }
         }
     };
@@ -831,7 +704,7 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
     for (int item = 0; item < n_items; ++item) {
         MRef r;
         m_item_n<kG>(L, item, r);
-        if (r.unit != cur.unit || r.pass != cur.pass) {
+        if (r.unit != cur.unit || r.pass != cur.pass || r.half != cur.half) {
             // new token operand: everything in flight lands first, so the
             // slice waits below stay exact
             wait_vm(0);
@@ -840,10 +713,25 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
             const int m = min(kMGroup, u.m - j0);
             live = 16 * tt < m;
             const int t = 16 * tt + (lane & 15);
+            const int tc = j0 + (t < m ? t : 0);
             const uint16_t* row;
-            if (kG) row = P.x + (int64_t)token_of(L, u, j0 + (t < m ? t : 0)) * kHidden;
-            else row = reinterpret_cast<const uint16_t*>(P.hp + u.h_off) +
-                       (int64_t)(j0 + (t < m ? t : 0)) * K;
+            if (kG) {
+                row = P.x + (int64_t)token_of(L, u, tc) * kHidden;
+            } else {
+                row = reinterpret_cast<const uint16_t*>(P.hp + u.h_off) +
+                      (int64_t)tc * gpairs_of(u) + r.half * kInter;
+                ep_ok = t < m;
+                ep_sh = u.expert < 0;
+                if (ep_sh) {
+                    ep_base = ((int64_t)tc * 2 + r.half) * kHidden;
+                    ep_w = 1.f;
+                } else {
+                    const int e = L.ent[u.tok0 + tc];
+                    const int tok = e / kTopK;
+                    ep_base = ((int64_t)tok * kSlots + (e - tok * kTopK)) * kPartWords;
+                    ep_w = P.weights[e];
+                }
+            }
 #pragma unroll
             for (int f = 0; f < KS; ++f) {
                 const int sl = kh + 2 * (f >> 3), ks = f & 7;
@@ -895,6 +783,10 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
                         for (int i = 0; i < 4; ++i) o[(rt * 4 + i) * kLanes] = acc[rt][i];
                 }
                 done = r;
+                dn_ok = ep_ok;
+                dn_sh = ep_sh;
+                dn_base = ep_base;
+                dn_w = ep_w;
             }
         }
     }
@@ -995,24 +887,6 @@ __device__ void v_items(const Params& P, Lds& L, uint32_t epoch) {
     }
 }
 
-// MFMA items of a phase, taken by the whole workgroup in order: the gate/up
-// and routed down items through m_stream, the shared down items (K = 2816)
-// one at a time through m_run.
-template <bool kG>
-__device__ void m_items(const Params& P, Lds& L, uint32_t epoch) {
-    if (kG) {
-        m_stream<true>(P, L, epoch);
-        return;
-    }
-    const Seg* S = L.dseg;
-    for (int s = 0; s < L.n_dseg; ++s) {
-        const Unit& u = L.unit[S[s].unit];
-        if (is_v(u.m)) continue;
-        const int pr = passes_of(u.m);
-        for (int i = S[s].lo; i < S[s].hi; ++i) d_item_m(P, L, u, i / pr, i % pr, epoch);
-    }
-}
-
 // x rows of this workgroup's VALU units of phase G into their LDS slots.
 __device__ void stage_x(const Params& P, Lds& L) {
     for (int s = 0; s < L.n_gseg; ++s) {
@@ -1027,11 +901,16 @@ __device__ void stage_x(const Params& P, Lds& L) {
     }
 }
 
-// Phase C: the 4T output words of this workgroup.
+// Phase C: the 4T output words of this workgroup. kSplit (two launches): the
+// shared expert's value of a row is bf16(lo + hi) of its two fp32 K-half
+// sums; otherwise it is the bf16 partial of slot 6.
+template <bool kSplit>
 __device__ void combine(const Params& P, uint32_t epoch) {
     Header* hdr = P.hdr;
     const int nw = P.T * (kPartWords / kWG);
+    constexpr int NS = kSplit ? kTopK : kSlots;
     const __amdgpu_buffer_rsrc_t rp = rsrc(P.part);
+    const __amdgpu_buffer_rsrc_t rs = rsrc(kSplit ? P.sp : P.part);
     for (int k = threadIdx.x; k < nw; k += kThreads) {
         const int g = blockIdx.x * nw + k;
         const int t = g / kPartWords, w = g - t * kPartWords;
@@ -1040,12 +919,20 @@ __device__ void combine(const Params& P, uint32_t epoch) {
         for (uint32_t it = 0; !ready; ++it) {
             ready = true;
 #pragma unroll
-            for (int s = 0; s < kSlots; ++s) {
+            for (int s = 0; s < NS; ++s) {
                 const int o = (((t * kSlots + s) * kPartWords) + w) * 8;
                 const uint2 v =
                     __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, o, 0, 16));
                 pay[s] = v.x;
                 ready &= v.y == epoch;
+            }
+            if (kSplit) {
+                // rows 2w, 2w + 1 of each K half: one 16-byte load of two words
+                const u32x4 lo = ld_dev16(rs, ((t * 2) * kHidden + 2 * w) * 8);
+                const u32x4 hi = ld_dev16(rs, ((t * 2 + 1) * kHidden + 2 * w) * 8);
+                ready &= lo.y == epoch && lo.w == epoch && hi.y == epoch && hi.w == epoch;
+                pay[kTopK] = pack_bf16(__uint_as_float(lo.x) + __uint_as_float(hi.x),
+                                       __uint_as_float(lo.z) + __uint_as_float(hi.z));
             }
             if (!ready) {
                 if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&hdr->abort) != 0)) {
@@ -1092,7 +979,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
     }
     __syncthreads();
     v_items<false>(P, L, epoch);
-    combine(P, epoch);
+    combine<false>(P, epoch);
     exit_epoch(hdr, epoch);
 }
 
@@ -1100,7 +987,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
 __global__ __launch_bounds__(kThreads, 1) void grouped_g_kernel(Params P) {
     __shared__ Lds L;
     build_tables(P, L);
-    m_items<true>(P, L, 0);
+    m_stream<true>(P, L, 0);
     stage_x(P, L);
     __syncthreads();
     v_items<true>(P, L, 0);
@@ -1112,14 +999,14 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_dc_kernel(Params P) {
     Header* hdr = P.hdr;
     const uint32_t epoch = ld_agent(&hdr->epoch) + 1u;
     build_tables(P, L);
-    m_items<false>(P, L, epoch);
+    m_stream<false>(P, L, epoch);
     for (int s = 0; s < L.n_dseg; ++s) {
         const Seg& sg = L.dseg[s];
         if (sg.stage >= 0) stage_h_plain(P, L.unit[sg.unit], L.stage + sg.stage);
     }
     __syncthreads();
     v_items<false>(P, L, epoch);
-    combine(P, epoch);
+    combine<true>(P, epoch);
     exit_epoch(hdr, epoch);
 }
 
@@ -1174,6 +1061,7 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
     P.hdr = reinterpret_cast<grouped::Header*>(ws);
     P.h = reinterpret_cast<uint64_t*>(ws + L.h);
     P.part = reinterpret_cast<uint64_t*>(ws + L.part);
+    P.sp = reinterpret_cast<uint64_t*>(ws + L.sp);
     P.T = n_tokens;
     if (n_tokens <= grouped::kVMax) {
         P.hp = nullptr;
