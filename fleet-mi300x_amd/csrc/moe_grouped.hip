@@ -163,23 +163,36 @@ __device__ __forceinline__ int d_rows_v(const Unit& u) {
     return u.expert < 0 ? (u.m > 4 ? 2 : 4) : (u.m > 4 ? 4 : 8);
 }
 
-// Items and their cost (G: 16 KB units; D: 11 KB units) of a unit. MFMA items
-// run pass-minor: item i is row block i / passes, token pass i % passes; the
-// shared expert's MFMA down items are two K halves of that sequence.
+// Items and their cost of a unit, in eighths of the time a one-token VALU
+// item takes per 16 KB (G) or 11 KB (D) of weight rows, as measured on the
+// DeepSeek-V2-Lite shapes with every CU streaming. A VALU item's time grows
+// with its tokens (dot products and the reduction per weight byte; fewer rows
+// in flight above 4 tokens in D); an MFMA item holds 8 units of weights, its
+// live token tiles load LDS and the matrix cores, and its operand load delays
+// its first copy. MFMA items run pass-minor: item i is row block i / passes,
+// token pass i % passes; the shared expert's MFMA down items are two K halves
+// of that sequence.
+__device__ __forceinline__ int m_tiles(int m) { return min(kMGroup / 16, (m + 15) >> 4); }
 __device__ __forceinline__ void g_items_of(const Unit& u, int& n, int& cost) {
     const int pairs = gpairs_of(u);
-    if (is_v(u.m)) { n = pairs / 2; cost = 1; }
-    else { n = 2 * pairs / kMRows * passes_of(u.m); cost = 8; }
+    if (is_v(u.m)) { n = pairs / 2; cost = u.m <= 4 ? 8 : 9; }
+    else {
+        n = 2 * pairs / kMRows * passes_of(u.m);
+        constexpr int kCost[4] = {84, 84, 99, 103};
+        cost = kCost[m_tiles(u.m) - 1];
+    }
 }
 __device__ __forceinline__ void d_items_of(const Unit& u, int& n, int& cost) {
     const bool sh = u.expert < 0;
     if (is_v(u.m)) {
         const int R = d_rows_v(u);
         n = kHidden / R;
-        cost = sh ? R / 2 : R / 4;
+        const int units = sh ? R / 2 : R / 4;            // 11 KB units of weights
+        cost = units * (u.m == 1 ? 8 : u.m == 2 ? 9 : u.m <= 4 ? 10 : 12);
     } else {
         n = (sh ? 2 : 1) * (kHidden / kMRows) * passes_of(u.m);
-        cost = 8;
+        constexpr int kCost[4] = {124, 132, 140, 150};
+        cost = kCost[m_tiles(u.m) - 1];
     }
 }
 
@@ -279,11 +292,15 @@ __device__ void build_tables(const Params& P, Lds& L) {
     __syncthreads();
     if (wave == 0) {
         const int c = L.cnt[lane];
-        const int pr = passes_of(c);           // 0 for an unselected expert
-        const bool v = c <= kVMax;
         // exclusive scans over the 64 experts: entry offsets, h words, costs
-        int s_off = c, s_h = c * (kInter / 2), s_g = (kInter / 2) * (c > 0 ? (v ? 1 : pr) : 0),
-            s_d = (kHidden / 4) * (c > 0 ? (v ? 1 : pr) : 0);
+        int s_off = c, s_h = c * (kInter / 2), s_g = 0, s_d = 0;
+        if (c > 0) {
+            int n, cost;
+            g_items_of(Unit{lane, c, 0, 0, 0, 0}, n, cost);
+            s_g = n * cost;
+            d_items_of(Unit{lane, c, 0, 0, 0, 0}, n, cost);
+            s_d = n * cost;
+        }
         const int e_off = s_off, e_h = s_h, e_g = s_g, e_d = s_d;
         s_off = wave_incl_scan(s_off);
         s_h = wave_incl_scan(s_h);
@@ -291,8 +308,11 @@ __device__ void build_tables(const Params& P, Lds& L) {
         s_d = wave_incl_scan(s_d);
         L.off[lane] = s_off - e_off;
         const unsigned long long sel = __ballot(c > 0);
-        const int vs = T <= kVMax ? 1 : passes_of(T);
-        const int g_sh = (kSharedInter / 2) * vs, d_sh = (kHidden / 2) * vs;
+        int g_sh, d_sh, n, cost;
+        g_items_of(Unit{-1, T, 0, 0, 0, 0}, n, cost);
+        g_sh = n * cost;
+        d_items_of(Unit{-1, T, 0, 0, 0, 0}, n, cost);
+        d_sh = n * cost;
         if (c > 0) {
             const int u = 1 + __builtin_popcountll(sel & ((1ull << lane) - 1ull));
             L.unit[u] = Unit{lane, c, s_off - e_off, T * (kSharedInter / 2) + s_h - e_h,
