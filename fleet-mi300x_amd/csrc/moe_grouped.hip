@@ -8,34 +8,34 @@
 // per token with the rounding of src/host/reference_decode.py:280-287.
 //
 // Launch shape. Work is cut into items that every workgroup takes from a
-// contiguous range holding 1/256 of the bytes, after building the dispatch
-// tables itself in LDS from the T x 6 ids (ballot-matched per-chunk counts, a
-// scan, stable positions): units = [shared expert (T tokens), then every
-// selected expert in id order (its tokens in token order)].
+// contiguous range holding 1/256 of the step's cost (items priced by their
+// measured time: VALU items by token count, MFMA items by live token tiles),
+// after building the dispatch tables itself in LDS from the T x 6 ids
+// (ballot-matched per-chunk counts, a scan, stable positions): units =
+// [shared expert (T tokens), then every selected expert in id order (its
+// tokens in token order)].
 //   * VALU units (<= 8 tokens): items of two gate/up row pairs (16 KB) or 2-8
 //     down rows; rows stream with 1 KB wave loads against the tokens' x / h
 //     held in LDS (dot2, one multi-value wave reduction per item), one item
 //     per wave from an LDS ticket.
 //   * MFMA units (> 8 tokens): items of 32 rows x up to 64 tokens taken by
-//     the whole workgroup, bf16 MFMA 16x16x32. Gate/up items stream
-//     (m_stream): each wave keeps its 16 tokens' x fragments for one K parity
-//     in registers, and the weight rows pass through a ring of 256-element K
+//     the whole workgroup, bf16 MFMA 16x16x32, all streamed (m_stream): each
+//     wave keeps its 16 tokens' x or h fragments for one K parity in
+//     registers, and the weight rows pass through a ring of 256-element K
 //     slices in LDS (global_load_lds, 1 KB per instruction, XOR-swizzled so
 //     the MFMA operand reads are conflict-free) kept 8 slices ahead across
-//     items. Down items (m_run) copy both the weight rows and the token rows
-//     of each slice to LDS, two slices in flight, one barrier per slice; wave
-//     w takes row tile w / 4 and token tile w % 4.
+//     items. The shared expert's down rows (K = 2816) run as two K halves
+//     whose fp32 sums the combine adds.
 // T <= 8 (every unit is a VALU unit): ONE launch, phases G (gate/up + SwiGLU)
 //   -> D (down) -> C (combine) handing data over through self-validating words
 //   (epoch << 32 | payload, device-scope stores and loads; no grid barrier).
 // T > 8: two launches on the stream, G, then D + C; h crosses the kernel
-//   boundary as plain bf16, so the MFMA down items load it with the same
-//   global_load_lds path as the weights.
-// Partials bf16(w * bf16(d)) (shared: bf16(d)) are published per (token,
-// slot) as tagged words of two rows; phase C sums them in slot order:
-// out[t] = bf16(bf16(sum_k part[t][k]) + part[t][shared]). The last
-// workgroup to exit advances the epoch. Every wait is bounded and records
-// FLEET_MOE_ABORT_GROUP_WAIT instead of hanging.
+//   boundary as plain bf16.
+// Partials bf16(w * bf16(d)) (shared: bf16(d), or with two launches the two
+// fp32 K-half sums) are published per (token, slot) as tagged words; phase C
+// sums them in slot order: out[t] = bf16(bf16(sum_k part[t][k]) + shared[t]).
+// The last workgroup to exit advances the epoch. Every wait is bounded and
+// records FLEET_MOE_ABORT_GROUP_WAIT instead of hanging.
 #include <stddef.h>
 
 #include "moe_common.h"
@@ -752,11 +752,13 @@ __device__ void m_stream(const Params& P, Lds& L, uint32_t epoch) {
                     ep_w = P.weights[e];
                 }
             }
+            // (a wave whose token tile holds no token of the pass loads none)
 #pragma unroll
             for (int f = 0; f < KS; ++f) {
                 const int sl = kh + 2 * (f >> 3), ks = f & 7;
                 const int e = kKs * sl + 32 * ks + 8 * (lane >> 4);
-                bf[f] = e < K ? *reinterpret_cast<const u32x4*>(row + e) : u32x4{0u, 0u, 0u, 0u};
+                bf[f] = live && e < K ? *reinterpret_cast<const u32x4*>(row + e)
+                                      : u32x4{0u, 0u, 0u, 0u};
             }
             // the operand is complete from here on (an explicit wait the
             // compiler accounts for, so it adds none before the MFMAs, where

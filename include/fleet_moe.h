@@ -125,7 +125,8 @@ size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, int32_t max
  * that), and out[t] = bf16(bf16(sum_k bf16(w[t][k] * E_{ids[t][k]}(x[t]))) +
  * shared(x[t])), the per-token combine of src/host/reference_decode.py:
  * 280-287, so grouped(T) equals T batch-1 MoE outputs up to fp32 summation
- * order. One launch over every CU (256 workgroups resident at once).
+ * order. One launch over every CU (256 workgroups resident at once) for
+ * n_tokens <= 8, two (gate/up, then down + combine) above that.
  * x_norm: bf16[n_tokens][hidden]; ids: int32[n_tokens][top_k] (each in
  * [0, n_routed), distinct per token); weights: fp32[n_tokens][top_k];
  * out: bf16[n_tokens][hidden]. 1 <= n_tokens <= max_tokens of the workspace
