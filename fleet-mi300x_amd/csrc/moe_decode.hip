@@ -406,6 +406,17 @@ __device__ bool wait_h(const Params& P, int unit, int n_chunks, uint32_t tag,
     }
 }
 
+// An LDS word read through inline asm: the compiler, which cannot tell the
+// word from the shared down rows the control wave copies into LDS by DMA,
+// would otherwise wait for every vector memory operation of the wave
+// (vmcnt(0)) before reading it. For words the DMA never writes.
+__device__ __forceinline__ int lds_word(const int* p) {
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int*)p;
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    return v;
+}
+
 // Any wave that needs the routing waits for the control wave's LDS
 // publication (bounded, because the control wave's own waits are bounded).
 __device__ __forceinline__ bool wait_routing(Lds& L) {
@@ -624,10 +635,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     const bool routed = wave < kTopK;
     const int unit = routed ? 1 + wave : 0;
     if (routed) {
-        wait_routing(L);
+        // the routing (published long before phase G ends) and this slot's
+        // expert, read without waiting for this wave's h stores
+        while (lds_word(&L.route) < 2) __builtin_amdgcn_s_sleep(1);
+        const int expert = __builtin_amdgcn_readfirstlane(lds_word(&L.ids[wave]));
         u32x4 W[24];
         const u32x4* base = reinterpret_cast<const u32x4*>(
-                                P.experts + (int64_t)L.ids[wave] * P.expert_stride +
+                                P.experts + (int64_t)expert * P.expert_stride +
                                 (int64_t)2 * kInter * kHidden) +
                             (int64_t)row0 * kInterChunks;
 #pragma unroll
