@@ -252,13 +252,18 @@ __device__ __forceinline__ void lds_wave_sync() {
 
 // ---------------------------------------------------------------- prologue
 
-// Dispatch tables and this workgroup's item ranges, all in LDS.
+// Dispatch tables and this workgroup's item ranges of the phases the launch
+// runs (kG: gate/up, kD: down), all in LDS.
+template <bool kG, bool kD>
 __device__ void build_tables(const Params& P, Lds& L) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kLanes - 1);
     const int T = P.T, N = T * kTopK;
     const int nchunks = (N + kLanes - 1) / kLanes;
     for (int i = tid; i < nchunks * kRouted; i += kThreads) (&L.pro.ccnt[0][0])[i] = 0;
-    if (tid == 0) { L.gnext = 0; L.dnext = 0; }
+    if (tid == 0) {
+        L.gnext = L.dnext = 0;
+        L.n_gseg = L.n_dseg = L.g_items = L.d_items = 0;   // a phase the launch skips stays empty
+    }
     __syncthreads();
     // per chunk of 64 entries: lanes with equal ids by 6 ballots; the rank of
     // an entry among them, and the count, kept by the lowest such lane
@@ -326,15 +331,20 @@ __device__ void build_tables(const Params& P, Lds& L) {
         }
     }
     __syncthreads();
-    for (int i = tid; i < N; i += kThreads) {
-        const int id = L.pro.id[i];
-        L.ent[L.off[id] + L.pro.ccnt[i >> 6][id] + L.pro.rank[i]] = (int16_t)i;
-    }
-    // this workgroup's item ranges: items whose first cost unit lies in
-    // [ceil(w C / 256), ceil((w + 1) C / 256)), over up to 65 units
-    if (wave == 0) {
+    if (wave != 0) {
+        // waves 1..7: sorted position -> entry
+        for (int i = tid - kLanes; i < N; i += kThreads - kLanes) {
+            const int id = L.pro.id[i];
+            L.ent[L.off[id] + L.pro.ccnt[i >> 6][id] + L.pro.rank[i]] = (int16_t)i;
+        }
+    } else {
+        // wave 0, meanwhile: this workgroup's item ranges, items whose first
+        // cost unit lies in [ceil(w C / 256), ceil((w + 1) C / 256)), over up
+        // to 65 units, and the LDS staging of their VALU units
         const int wg = blockIdx.x;
+#pragma unroll
         for (int ph = 0; ph < 2; ++ph) {
+            if (ph == 0 ? !kG : !kD) continue;
             const int C = ph == 0 ? L.g_total : L.d_total;
             const int lo = (wg * C + kWG - 1) / kWG, hi = ((wg + 1) * C + kWG - 1) / kWG;
             Seg* S = ph == 0 ? L.gseg : L.dseg;
@@ -356,34 +366,30 @@ __device__ void build_tables(const Params& P, Lds& L) {
                 const int si = ns + __builtin_popcountll(sm & ((1ull << lane) - 1ull));
                 const int items = seg ? i1 - i0 : 0;
                 const int incl = wave_incl_scan(items);
-                if (seg && si < kSegMax) S[si] = Seg{ui, i0, i1, nitems + incl - items, -1};
+                if (seg && si < kSegMax) {
+                    // staging bytes of a VALU unit's x (G) or h (D) rows
+                    const Unit& u = L.unit[ui];
+                    const int need = !is_v(u.m) ? 0 : ph == 0 ? u.m * kHidden * 2
+                                                                : u.m * gpairs_of(u) * 2;
+                    S[si] = Seg{ui, i0, i1, nitems + incl - items, need};
+                }
                 ns += __builtin_popcountll(sm);
                 nitems += __builtin_amdgcn_readlane(incl, kLanes - 1);
             }
+            const int nseg = min(ns, kSegMax);
             if (lane == 0) {
                 if (ns > kSegMax) flag_abort(P.hdr, kAbortStage);
-                if (ph == 0) { L.n_gseg = min(ns, kSegMax); L.g_items = nitems; }
-                else { L.n_dseg = min(ns, kSegMax); L.d_items = nitems; }
+                if (ph == 0) { L.n_gseg = nseg; L.g_items = nitems; }
+                else { L.n_dseg = nseg; L.d_items = nitems; }
             }
-        }
-        lds_wave_sync();
-        if (lane == 0) {
-            // LDS staging for the VALU units of each phase
-            int at = 0;
-            for (int s = 0; s < L.n_gseg; ++s) {
-                const Unit& un = L.unit[L.gseg[s].unit];
-                if (!is_v(un.m)) continue;
-                const int need = un.m * kHidden * 2;
-                if (at + need <= kStageBytes) { L.gseg[s].stage = at; at += need; }
-                else flag_abort(P.hdr, kAbortStage);
-            }
-            at = 0;
-            for (int s = 0; s < L.n_dseg; ++s) {
-                const Unit& un = L.unit[L.dseg[s].unit];
-                if (!is_v(un.m)) continue;
-                const int need = un.m * gpairs_of(un) * 2;
-                if (at + need <= kStageBytes) { L.dseg[s].stage = at; at += need; }
-                else flag_abort(P.hdr, kAbortStage);
+            lds_wave_sync();
+            // lane s < nseg: its segment's staging offset (a running sum in
+            // segment order), or -1 for an MFMA unit
+            const int need = lane < nseg ? S[lane].stage : 0;
+            const int end = wave_incl_scan(need);
+            if (lane < nseg) {
+                if (need > 0 && end > kStageBytes) flag_abort(P.hdr, kAbortStage);
+                S[lane].stage = need > 0 && end <= kStageBytes ? end - need : -1;
             }
         }
     }
@@ -990,7 +996,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
     __shared__ Lds L;
     Header* hdr = P.hdr;
     const uint32_t epoch = ld_agent(&hdr->epoch) + 1u;
-    build_tables(P, L);
+    build_tables<true, true>(P, L);
     stage_x(P, L);
     __syncthreads();
     v_items<true>(P, L, epoch);
@@ -1008,7 +1014,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
 // T > 8, launch 1: phase G, h as plain words.
 __global__ __launch_bounds__(kThreads, 1) void grouped_g_kernel(Params P) {
     __shared__ Lds L;
-    build_tables(P, L);
+    build_tables<true, false>(P, L);
     m_stream<true>(P, L, 0);
     stage_x(P, L);
     __syncthreads();
@@ -1020,7 +1026,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_dc_kernel(Params P) {
     __shared__ Lds L;
     Header* hdr = P.hdr;
     const uint32_t epoch = ld_agent(&hdr->epoch) + 1u;
-    build_tables(P, L);
+    build_tables<false, true>(P, L);
     m_stream<false>(P, L, epoch);
     for (int s = 0; s < L.n_dseg; ++s) {
         const Seg& sg = L.dseg[s];
