@@ -86,15 +86,20 @@ struct Header {
 };
 static_assert(offsetof(Header, abort) == 8, "status word offset");
 
+// The dispatch tables launch 1 of a two-launch step leaves for launch 2
+// (struct Tab below): three counts, the units, the sorted entries.
+constexpr int kTabBytes = 16 + kUnitsMax * 6 * 4 + kMaxEntries * 2;
+
 struct Layout {
-    size_t h, hp, part, sp, total;
+    size_t tab, h, hp, part, sp, total;
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 __host__ __device__ inline Layout layout(int max_tokens) {
     Layout L;
-    L.h = align256(sizeof(Header));
+    L.tab = align256(sizeof(Header));
+    L.h = L.tab + align256(kTabBytes);
     L.hp = L.h + align256((size_t)(max_tokens < kVMax ? max_tokens : kVMax) * kHWordsPerToken * 8);
     L.part = L.hp + align256((size_t)max_tokens * kHWordsPerToken * 4);
     L.sp = L.part + align256((size_t)max_tokens * kSlots * kPartWords * 8);
@@ -115,6 +120,7 @@ struct Params {
     uint32_t* hp;              // plain h words, two bf16 each (two launches)
     uint64_t* part;            // tagged partial words [T][7][1024]
     uint64_t* sp;              // tagged fp32 shared down sums [T][2 K halves][2048] (two launches)
+    struct Tab* tab;           // dispatch tables handed from launch 1 to launch 2
     int T;
 };
 
@@ -126,6 +132,13 @@ struct Unit {
     int gstart;     // first G cost unit
     int dstart;     // first D cost unit
 };
+
+struct Tab {
+    int n_units, g_total, d_total, pad;
+    Unit unit[kUnitsMax];
+    int16_t ent[kMaxEntries];
+};
+static_assert(sizeof(Tab) <= kTabBytes && sizeof(Unit) == 6 * 4, "table blob");
 
 struct Seg {
     int unit, lo, hi, base;   // items [lo, hi) of the unit; base = first ticket
@@ -252,6 +265,66 @@ __device__ __forceinline__ void lds_wave_sync() {
 
 // ---------------------------------------------------------------- prologue
 
+// Wave 0: this workgroup's item ranges of the phases the launch runs (kG:
+// gate/up, kD: down), items whose first cost unit lies in [ceil(w C / 256),
+// ceil((w + 1) C / 256)), over up to 65 units, and the LDS staging of their
+// VALU units (the units must be in LDS).
+template <bool kG, bool kD>
+__device__ void item_ranges(const Params& P, Lds& L) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wg = blockIdx.x;
+#pragma unroll
+    for (int ph = 0; ph < 2; ++ph) {
+        if (ph == 0 ? !kG : !kD) continue;
+        const int C = ph == 0 ? L.g_total : L.d_total;
+        const int lo = (wg * C + kWG - 1) / kWG, hi = ((wg + 1) * C + kWG - 1) / kWG;
+        Seg* S = ph == 0 ? L.gseg : L.dseg;
+        int ns = 0, nitems = 0;
+        for (int r0 = 0; r0 < L.n_units; r0 += kLanes) {
+            const int ui = r0 + lane;
+            const bool have = ui < L.n_units;
+            int n = 0, cost = 1, start = 0;
+            if (have) {
+                const Unit& u = L.unit[ui];
+                if (ph == 0) { g_items_of(u, n, cost); start = u.gstart; }
+                else { d_items_of(u, n, cost); start = u.dstart; }
+            }
+            const int a = lo - start, b = hi - start;
+            const int i0 = a <= 0 ? 0 : min(n, (a + cost - 1) / cost);
+            const int i1 = b <= 0 ? 0 : min(n, (b + cost - 1) / cost);
+            const bool seg = have && i0 < i1;
+            const unsigned long long sm = __ballot(seg);
+            const int si = ns + __builtin_popcountll(sm & ((1ull << lane) - 1ull));
+            const int items = seg ? i1 - i0 : 0;
+            const int incl = wave_incl_scan(items);
+            if (seg && si < kSegMax) {
+                // staging bytes of a VALU unit's x (G) or h (D) rows
+                const Unit& u = L.unit[ui];
+                const int need = !is_v(u.m) ? 0 : ph == 0 ? u.m * kHidden * 2
+                                                            : u.m * gpairs_of(u) * 2;
+                S[si] = Seg{ui, i0, i1, nitems + incl - items, need};
+            }
+            ns += __builtin_popcountll(sm);
+            nitems += __builtin_amdgcn_readlane(incl, kLanes - 1);
+        }
+        const int nseg = min(ns, kSegMax);
+        if (lane == 0) {
+            if (ns > kSegMax) flag_abort(P.hdr, kAbortStage);
+            if (ph == 0) { L.n_gseg = nseg; L.g_items = nitems; }
+            else { L.n_dseg = nseg; L.d_items = nitems; }
+        }
+        lds_wave_sync();
+        // lane s < nseg: its segment's staging offset (a running sum in
+        // segment order), or -1 for an MFMA unit
+        const int need = lane < nseg ? S[lane].stage : 0;
+        const int end = wave_incl_scan(need);
+        if (lane < nseg) {
+            if (need > 0 && end > kStageBytes) flag_abort(P.hdr, kAbortStage);
+            S[lane].stage = need > 0 && end <= kStageBytes ? end - need : -1;
+        }
+    }
+}
+
 // Dispatch tables and this workgroup's item ranges of the phases the launch
 // runs (kG: gate/up, kD: down), all in LDS.
 template <bool kG, bool kD>
@@ -338,61 +411,45 @@ __device__ void build_tables(const Params& P, Lds& L) {
             L.ent[L.off[id] + L.pro.ccnt[i >> 6][id] + L.pro.rank[i]] = (int16_t)i;
         }
     } else {
-        // wave 0, meanwhile: this workgroup's item ranges, items whose first
-        // cost unit lies in [ceil(w C / 256), ceil((w + 1) C / 256)), over up
-        // to 65 units, and the LDS staging of their VALU units
-        const int wg = blockIdx.x;
-#pragma unroll
-        for (int ph = 0; ph < 2; ++ph) {
-            if (ph == 0 ? !kG : !kD) continue;
-            const int C = ph == 0 ? L.g_total : L.d_total;
-            const int lo = (wg * C + kWG - 1) / kWG, hi = ((wg + 1) * C + kWG - 1) / kWG;
-            Seg* S = ph == 0 ? L.gseg : L.dseg;
-            int ns = 0, nitems = 0;
-            for (int r0 = 0; r0 < L.n_units; r0 += kLanes) {
-                const int ui = r0 + lane;
-                const bool have = ui < L.n_units;
-                int n = 0, cost = 1, start = 0;
-                if (have) {
-                    const Unit& u = L.unit[ui];
-                    if (ph == 0) { g_items_of(u, n, cost); start = u.gstart; }
-                    else { d_items_of(u, n, cost); start = u.dstart; }
-                }
-                const int a = lo - start, b = hi - start;
-                const int i0 = a <= 0 ? 0 : min(n, (a + cost - 1) / cost);
-                const int i1 = b <= 0 ? 0 : min(n, (b + cost - 1) / cost);
-                const bool seg = have && i0 < i1;
-                const unsigned long long sm = __ballot(seg);
-                const int si = ns + __builtin_popcountll(sm & ((1ull << lane) - 1ull));
-                const int items = seg ? i1 - i0 : 0;
-                const int incl = wave_incl_scan(items);
-                if (seg && si < kSegMax) {
-                    // staging bytes of a VALU unit's x (G) or h (D) rows
-                    const Unit& u = L.unit[ui];
-                    const int need = !is_v(u.m) ? 0 : ph == 0 ? u.m * kHidden * 2
-                                                                : u.m * gpairs_of(u) * 2;
-                    S[si] = Seg{ui, i0, i1, nitems + incl - items, need};
-                }
-                ns += __builtin_popcountll(sm);
-                nitems += __builtin_amdgcn_readlane(incl, kLanes - 1);
-            }
-            const int nseg = min(ns, kSegMax);
-            if (lane == 0) {
-                if (ns > kSegMax) flag_abort(P.hdr, kAbortStage);
-                if (ph == 0) { L.n_gseg = nseg; L.g_items = nitems; }
-                else { L.n_dseg = nseg; L.d_items = nitems; }
-            }
-            lds_wave_sync();
-            // lane s < nseg: its segment's staging offset (a running sum in
-            // segment order), or -1 for an MFMA unit
-            const int need = lane < nseg ? S[lane].stage : 0;
-            const int end = wave_incl_scan(need);
-            if (lane < nseg) {
-                if (need > 0 && end > kStageBytes) flag_abort(P.hdr, kAbortStage);
-                S[lane].stage = need > 0 && end <= kStageBytes ? end - need : -1;
-            }
-        }
+        // wave 0, meanwhile: this workgroup's item ranges
+        item_ranges<kG, kD>(P, L);
     }
+    __syncthreads();
+}
+
+// Launch 1 of a two-launch step (workgroup 0): the tables every workgroup
+// built alike, for launch 2 (the kernel boundary orders the stores before
+// launch 2's loads).
+__device__ void store_tables(const Params& P, const Lds& L) {
+    Tab* tb = P.tab;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        tb->n_units = L.n_units;
+        tb->g_total = L.g_total;
+        tb->d_total = L.d_total;
+    }
+    for (int i = tid; i < kUnitsMax * 6; i += kThreads)
+        reinterpret_cast<int*>(tb->unit)[i] = reinterpret_cast<const int*>(L.unit)[i];
+    for (int i = tid; i < P.T * kTopK; i += kThreads) tb->ent[i] = L.ent[i];
+}
+
+// Launch 2: launch 1's tables, then this launch's item ranges.
+template <bool kG, bool kD>
+__device__ void load_tables(const Params& P, Lds& L) {
+    const Tab* tb = P.tab;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        L.gnext = L.dnext = 0;
+        L.n_gseg = L.n_dseg = L.g_items = L.d_items = 0;
+        L.n_units = tb->n_units;
+        L.g_total = tb->g_total;
+        L.d_total = tb->d_total;
+    }
+    for (int i = tid; i < kUnitsMax * 6; i += kThreads)
+        reinterpret_cast<int*>(L.unit)[i] = reinterpret_cast<const int*>(tb->unit)[i];
+    for (int i = tid; i < P.T * kTopK; i += kThreads) L.ent[i] = tb->ent[i];
+    __syncthreads();
+    if (tid < kLanes) item_ranges<kG, kD>(P, L);
     __syncthreads();
 }
 
@@ -1015,6 +1072,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
 __global__ __launch_bounds__(kThreads, 1) void grouped_g_kernel(Params P) {
     __shared__ Lds L;
     build_tables<true, false>(P, L);
+    if (blockIdx.x == 0) store_tables(P, L);
     m_stream<true>(P, L, 0);
     stage_x(P, L);
     __syncthreads();
@@ -1026,7 +1084,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_dc_kernel(Params P) {
     __shared__ Lds L;
     Header* hdr = P.hdr;
     const uint32_t epoch = ld_agent(&hdr->epoch) + 1u;
-    build_tables<false, true>(P, L);
+    load_tables<false, true>(P, L);
     m_stream<false>(P, L, epoch);
     for (int s = 0; s < L.n_dseg; ++s) {
         const Seg& sg = L.dseg[s];
@@ -1090,6 +1148,7 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
     P.h = reinterpret_cast<uint64_t*>(ws + L.h);
     P.part = reinterpret_cast<uint64_t*>(ws + L.part);
     P.sp = reinterpret_cast<uint64_t*>(ws + L.sp);
+    P.tab = reinterpret_cast<grouped::Tab*>(ws + L.tab);
     P.T = n_tokens;
     if (n_tokens <= grouped::kVMax) {
         P.hp = nullptr;
