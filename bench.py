@@ -104,7 +104,8 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the MoE decode path runs on one GPU, see DESIGN.md for how it would shard)",
+              "(the MoE decode path runs on one GPU; across GPUs its experts would shard "
+              "by id, with one all-to-all of the 4 KB hidden vector each way per layer)",
               file=sys.stderr)
         return 2
     import torch
