@@ -188,7 +188,7 @@ __device__ __forceinline__ int d_rows_v(const Unit& u) {
 __device__ __forceinline__ int m_tiles(int m) { return min(kMGroup / 16, (m + 15) >> 4); }
 __device__ __forceinline__ void g_items_of(const Unit& u, int& n, int& cost) {
     const int pairs = gpairs_of(u);
-    if (is_v(u.m)) { n = pairs / 2; cost = u.m <= 4 ? 8 : 9; }
+    if (is_v(u.m)) { n = pairs / 2; cost = u.m <= 3 ? 8 : 9; }
     else {
         n = 2 * pairs / kMRows * passes_of(u.m);
         constexpr int kCost[4] = {84, 84, 99, 103};
