@@ -991,6 +991,7 @@ using namespace fleet_moe;
 
 int fleet_moe_check_dims(const fleet_moe_dims* d);
 int fleet_moe_check_device(int min_cus);
+int fleet_moe_check_resident(const void* fn, int threads, int grid);
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -1023,7 +1024,9 @@ extern "C" int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, 
         !aligned(rope_cos, 4) || !aligned(rope_sin, 4))
         return FLEET_MOE_ERR_ARG;
     if (workspace_bytes < sizeof(attn::Workspace)) return FLEET_MOE_ERR_WORKSPACE;
-    if (int e = fleet_moe_check_device(attn::kWG)) return e;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&attn::attn_layer_kernel),
+                                         attn::kThreads, attn::kWG))
+        return e;
     attn::Params P;
     P.x = x;
     P.x_out = x_out;

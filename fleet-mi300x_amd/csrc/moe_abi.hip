@@ -34,8 +34,8 @@ std::mutex g_mu;
 std::vector<DeviceInfo> g_dev;
 }  // namespace
 
-// Per device, once: the code object is gfx950-only, and the decode kernel
-// needs a cooperative launch of `min_cus` resident workgroups.
+// Per device, once: the code object is gfx950-only, and the kernels whose
+// workgroups wait on each other launch one workgroup per CU over `min_cus` CUs.
 int check_device_impl(int min_cus) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -47,16 +47,44 @@ int check_device_impl(int min_cus) {
         hipDeviceProp_t prop;
         e = hipGetDeviceProperties(&prop, dev);
         if (e != hipSuccess) return (int)e;
-        int coop = 0;
-        e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
-        if (e != hipSuccess) return (int)e;
-        di.status = (strncmp(prop.gcnArchName, "gfx950", 6) == 0 && coop &&
+        di.status = (strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
                      prop.multiProcessorCount >= min_cus)
                         ? 0
                         : FLEET_MOE_ERR_DEVICE;
         di.checked = 1;
     }
     return di.status;
+}
+
+namespace {
+struct ResidentInfo {
+    int dev;
+    const void* fn;
+    int status;
+};
+std::vector<ResidentInfo> g_resident;
+}  // namespace
+
+// Per device and kernel, once: the kernel's workgroups wait for each other's
+// data, so all `grid` of them (one per CU, `threads` threads each) must be
+// resident at the same time. That holds when the device has at least `grid`
+// CUs and one workgroup fits on a CU with the kernel's registers and LDS;
+// otherwise FLEET_MOE_ERR_DEVICE. (Work of other processes or streams holding
+// CUs can still delay residency; the kernels' waits are bounded for that.)
+int check_resident_impl(const void* fn, int threads, int grid) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (int st = check_device_impl(grid)) return st;
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (const ResidentInfo& r : g_resident)
+        if (r.dev == dev && r.fn == fn) return r.status;
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0);
+    if (e != hipSuccess) return (int)e;
+    const int st = per_cu >= 1 ? 0 : FLEET_MOE_ERR_DEVICE;
+    g_resident.push_back(ResidentInfo{dev, fn, st});
+    return st;
 }
 
 namespace router {
@@ -157,6 +185,9 @@ using namespace fleet_moe;
 
 int fleet_moe_check_dims(const fleet_moe_dims* d) { return check_dims_impl(d); }
 int fleet_moe_check_device(int min_cus) { return check_device_impl(min_cus); }
+int fleet_moe_check_resident(const void* fn, int threads, int grid) {
+    return check_resident_impl(fn, threads, grid);
+}
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -216,7 +247,8 @@ extern "C" const char* fleet_moe_error_string(int code) {
         case FLEET_MOE_ERR_ARG: return "fleet_moe: null, misaligned or out-of-range argument";
         case FLEET_MOE_ERR_WORKSPACE: return "fleet_moe: workspace too small";
         case FLEET_MOE_ERR_DEVICE:
-            return "fleet_moe: device is not a gfx950 with cooperative launch and enough CUs";
+            return "fleet_moe: device is not a gfx950 with enough CUs to hold one workgroup of "
+                   "the kernel on each";
         default: return hipGetErrorString((hipError_t)code);
     }
 }

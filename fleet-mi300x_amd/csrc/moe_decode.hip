@@ -802,6 +802,7 @@ static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 int fleet_moe_check_dims(const fleet_moe_dims* d);   // moe_abi.hip
 int fleet_moe_check_device(int min_cus);              // moe_abi.hip
+int fleet_moe_check_resident(const void* fn, int threads, int grid);
 
 #if FLEET_MOE_TRACE
 static unsigned long long* g_trace = nullptr;
@@ -830,7 +831,9 @@ extern "C" int fleet_moe_layer_decode(const fleet_moe_layer* layer, const float*
     if (layer->expert_stride < kExpertStride || layer->expert_stride % kChunk != 0)
         return FLEET_MOE_ERR_DIMS;
     if (workspace_bytes < fleet_moe_layer_workspace_bytes(dims)) return FLEET_MOE_ERR_WORKSPACE;
-    if (int e = fleet_moe_check_device(decode::kWG)) return e;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&decode::moe_decode_kernel),
+                                         decode::kThreads, decode::kWG))
+        return e;
 
     decode::Params P;
     P.norm = layer->norm;

@@ -258,6 +258,7 @@ using namespace fleet_moe;
 
 int fleet_moe_check_dims(const fleet_moe_dims* d);
 int fleet_moe_check_device(int min_cus);
+int fleet_moe_check_resident(const void* fn, int threads, int grid);
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -277,7 +278,9 @@ extern "C" int fleet_moe_dense_decode(const uint16_t* norm, const uint16_t* w, i
         (norm && !aligned(norm, 8)) || (mlp_out && !aligned(mlp_out, 2)))
         return FLEET_MOE_ERR_ARG;
     if (workspace_bytes < sizeof(dense::Workspace)) return FLEET_MOE_ERR_WORKSPACE;
-    if (int e = fleet_moe_check_device(dense::kWG)) return e;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&dense::dense_kernel),
+                                         dense::kThreads, dense::kWG))
+        return e;
     dense::Params P;
     P.norm = norm;
     P.w = w;

@@ -94,10 +94,10 @@ struct Layout {
     size_t tab, h, hp, part, sp, total;
 };
 
-__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+__host__ __device__ constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-__host__ __device__ inline Layout layout(int max_tokens) {
-    Layout L;
+__host__ __device__ constexpr Layout layout(int max_tokens) {
+    Layout L{};
     L.tab = align256(sizeof(Header));
     L.h = L.tab + align256(kTabBytes);
     L.hp = L.h + align256((size_t)(max_tokens < kVMax ? max_tokens : kVMax) * kHWordsPerToken * 8);
@@ -121,6 +121,7 @@ struct Params {
     uint64_t* part;            // tagged partial words [T][7][1024]
     uint64_t* sp;              // tagged fp32 shared down sums [T][2 K halves][2048] (two launches)
     struct Tab* tab;           // dispatch tables handed from launch 1 to launch 2
+    size_t ws_tail16;          // 16-byte words of the workspace after the header
     int T;
 };
 
@@ -211,6 +212,13 @@ __device__ __forceinline__ void d_items_of(const Unit& u, int& n, int& cost) {
 
 __device__ __forceinline__ void flag_abort(Header* hdr, uint32_t bit) {
     __hip_atomic_fetch_or(&hdr->abort, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A wait gives up early once another wait of the step has expired (or the
+// staging bound was hit, which leaves work undone); the id warning bit does
+// not stop anything.
+__device__ __forceinline__ bool step_failed(Header* hdr) {
+    return (ld_agent(&hdr->abort) & (FLEET_MOE_ABORT_GROUP_WAIT | kAbortStage)) != 0;
 }
 
 __device__ __forceinline__ void st_word(uint64_t* p, uint32_t epoch, uint32_t payload) {
@@ -343,8 +351,11 @@ __device__ void build_tables(const Params& P, Lds& L) {
     for (int c = wave; c < nchunks; c += kWaves) {
         const int i = c * kLanes + lane;
         const bool valid = i < N;
-        const int id = valid ? min(max(P.ids[i], 0), kRouted - 1) : 0;
+        const int raw = valid ? P.ids[i] : 0;
+        const int id = min(max(raw, 0), kRouted - 1);   // clamped: addresses stay in bounds
         if (valid) L.pro.id[i] = (int8_t)id;
+        if (__ballot(raw != id) && lane == 0 && blockIdx.x == 0)
+            flag_abort(P.hdr, FLEET_MOE_ABORT_BAD_ID);
         unsigned long long same = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 6; ++b) {
@@ -903,8 +914,7 @@ __device__ bool poll_h(const Params& P, const Unit& u, int j0, int m, uint8_t* s
         for (;; ++it) {
             v = ld_dev16(rs, 16 * k);
             if (v.y == epoch && v.w == epoch) break;
-            if (it >= kSpinLimit ||
-                ((it & 1023) == 1023 && ld_agent(&P.hdr->abort) != 0)) {
+            if (it >= kSpinLimit || ((it & 1023) == 1023 && step_failed(P.hdr))) {
                 ok = false;
                 break;
             }
@@ -1020,7 +1030,7 @@ __device__ void combine(const Params& P, uint32_t epoch) {
                                        __uint_as_float(lo.z) + __uint_as_float(hi.z));
             }
             if (!ready) {
-                if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&hdr->abort) != 0)) {
+                if (it >= kSpinLimit || ((it & 1023) == 1023 && step_failed(hdr))) {
                     flag_abort(hdr, FLEET_MOE_ABORT_GROUP_WAIT);
                     break;
                 }
@@ -1039,12 +1049,33 @@ __device__ void combine(const Params& P, uint32_t epoch) {
     }
 }
 
-__device__ __forceinline__ void exit_epoch(Header* hdr, uint32_t epoch) {
+// The last workgroup to exit publishes the epoch the next call starts from.
+// After the call numbered 2^32 - 1 the tags would wrap (and tag 0 is what a
+// zero-filled word carries), so that workgroup first clears every tagged word
+// and restarts the count from 0, which leaves the workspace as it was when
+// new; the next launch on the stream starts after this one has finished.
+__device__ void exit_epoch(const Params& P, uint32_t epoch) {
+    __shared__ int s_last;
+    Header* hdr = P.hdr;
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t old = __hip_atomic_fetch_add(&hdr->exits, 1u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&hdr->epoch, epoch);
+        s_last = old + 1u == epoch * (uint32_t)kWG;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (epoch != 0xffffffffu) {
+        if (threadIdx.x == 0) st_agent(&hdr->epoch, epoch);
+        return;
+    }
+    u32x4* w = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(hdr) + sizeof(Header));
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (size_t i = threadIdx.x; i < P.ws_tail16; i += kThreads) w[i] = z;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st_agent(&hdr->exits, 0u);
+        st_agent(&hdr->epoch, 0u);
     }
 }
 
@@ -1065,7 +1096,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
     __syncthreads();
     v_items<false>(P, L, epoch);
     combine<false>(P, epoch);
-    exit_epoch(hdr, epoch);
+    exit_epoch(P, epoch);
 }
 
 // T > 8, launch 1: phase G, h as plain words.
@@ -1093,7 +1124,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_dc_kernel(Params P) {
     __syncthreads();
     v_items<false>(P, L, epoch);
     combine<true>(P, epoch);
-    exit_epoch(hdr, epoch);
+    exit_epoch(P, epoch);
 }
 
 }  // namespace grouped
@@ -1103,6 +1134,7 @@ using namespace fleet_moe;
 
 int fleet_moe_check_dims(const fleet_moe_dims* d);
 int fleet_moe_check_device(int min_cus);
+int fleet_moe_check_resident(const void* fn, int threads, int grid);
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -1112,30 +1144,42 @@ extern "C" size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, 
     return grouped::layout(max_tokens).total;
 }
 
-extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
-                                 const int32_t* ids, const float* weights,
-                                 const uint16_t* x_norm, uint16_t* out, void* workspace,
-                                 size_t workspace_bytes, const fleet_moe_dims* dims,
-                                 hipStream_t stream) {
+// Argument checks shared by both entry points (everything but the workspace).
+static int check_grouped_args(const fleet_moe_layer* layer, int32_t n_tokens, const int32_t* ids,
+                              const float* weights, const uint16_t* x_norm, uint16_t* out,
+                              const fleet_moe_dims* dims) {
     if (!layer || !dims) return FLEET_MOE_ERR_ARG;
     if (int e = fleet_moe_check_dims(dims)) return e;
-    if (!layer->experts || !layer->shared || !ids || !weights || !x_norm || !out || !workspace)
+    if (!layer->experts || !layer->shared || !ids || !weights || !x_norm || !out)
         return FLEET_MOE_ERR_ARG;
     if (n_tokens < 1 || n_tokens > grouped::kMaxTokens) return FLEET_MOE_ERR_ARG;
     if (!aligned(layer->experts, 16) || !aligned(layer->shared, 16) || !aligned(x_norm, 16) ||
-        !aligned(out, 4) || !aligned(ids, 4) || !aligned(weights, 4) || !aligned(workspace, 256))
+        !aligned(out, 4) || !aligned(ids, 4) || !aligned(weights, 4))
         return FLEET_MOE_ERR_ARG;
     if (layer->expert_stride < kExpertStride || layer->expert_stride % kChunk != 0)
         return FLEET_MOE_ERR_DIMS;
-    // The workspace is laid out for the max_tokens it was sized for; recover it.
-    int max_tokens = 0;
-    for (int t = grouped::kMaxTokens; t >= 1; --t)
-        if (grouped::layout(t).total <= workspace_bytes) { max_tokens = t; break; }
-    if (max_tokens < n_tokens) return FLEET_MOE_ERR_WORKSPACE;
-    if (int e = fleet_moe_check_device(grouped::kWG)) return e;
+    return 0;
+}
 
+// Every grouped kernel waits on other workgroups (tagged words) except launch
+// 1 of a two-launch step; all three are checked so either plan can run.
+static int check_grouped_resident() {
+    using namespace grouped;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&grouped_fused_kernel),
+                                         kThreads, kWG))
+        return e;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&grouped_g_kernel),
+                                         kThreads, kWG))
+        return e;
+    return fleet_moe_check_resident(reinterpret_cast<const void*>(&grouped_dc_kernel), kThreads,
+                                    kWG);
+}
+
+// Enqueue the step on a workspace laid out for `max_tokens` (arguments checked).
+static int launch_grouped(const fleet_moe_layer* layer, int32_t n_tokens, const int32_t* ids,
+                          const float* weights, const uint16_t* x_norm, uint16_t* out,
+                          char* ws, int max_tokens, hipStream_t stream) {
     const grouped::Layout L = grouped::layout(max_tokens);
-    char* ws = static_cast<char*>(workspace);
     grouped::Params P;
     P.experts = layer->experts;
     P.shared = layer->shared;
@@ -1149,6 +1193,7 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
     P.part = reinterpret_cast<uint64_t*>(ws + L.part);
     P.sp = reinterpret_cast<uint64_t*>(ws + L.sp);
     P.tab = reinterpret_cast<grouped::Tab*>(ws + L.tab);
+    P.ws_tail16 = (L.total - sizeof(grouped::Header)) / 16;
     P.T = n_tokens;
     if (n_tokens <= grouped::kVMax) {
         P.hp = nullptr;
@@ -1163,3 +1208,21 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
     }
     return (int)hipGetLastError();
 }
+
+extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
+                                 const int32_t* ids, const float* weights,
+                                 const uint16_t* x_norm, uint16_t* out, void* workspace,
+                                 size_t workspace_bytes, const fleet_moe_dims* dims,
+                                 hipStream_t stream) {
+    if (int e = check_grouped_args(layer, n_tokens, ids, weights, x_norm, out, dims)) return e;
+    if (!workspace || !aligned(workspace, 256)) return FLEET_MOE_ERR_ARG;
+    // The workspace is laid out for the max_tokens it was sized for; recover it.
+    int max_tokens = 0;
+    for (int t = grouped::kMaxTokens; t >= 1; --t)
+        if (grouped::layout(t).total <= workspace_bytes) { max_tokens = t; break; }
+    if (max_tokens < n_tokens) return FLEET_MOE_ERR_WORKSPACE;
+    if (int e = check_grouped_resident()) return e;
+    return launch_grouped(layer, n_tokens, ids, weights, x_norm, out,
+                          static_cast<char*>(workspace), max_tokens, stream);
+}
+

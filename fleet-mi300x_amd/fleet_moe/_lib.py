@@ -22,6 +22,7 @@ ABORT_GROUP_WAIT = 0x4
 ABORT_POSITION = 0x8
 ABORT_TOKEN = 0x10
 ABORT_ATTN_WAIT = 0x20
+ABORT_BAD_ID = 0x40
 
 
 class FleetMoeDims(ctypes.Structure):

@@ -89,8 +89,12 @@ size_t fleet_moe_layer_workspace_bytes(const fleet_moe_dims* dims);
  * residual add) with the selection rule above.
  * x: fp32[hidden]; x_out: fp32[hidden] (may equal x); moe_out: bf16[hidden]
  * (the MoE output before the residual add) or NULL; ids: int32[top_k] or
- * NULL; weights: fp32[top_k] or NULL. Launches one cooperative kernel over
- * every CU of the device. */
+ * NULL; weights: fp32[top_k] or NULL. One launch of 256 workgroups (one per
+ * CU) that hand data to each other through the workspace, so all of them must
+ * be resident at once: the entry point checks once per device that the device
+ * has >= 256 CUs and that one workgroup of the kernel fits on a CU
+ * (FLEET_MOE_ERR_DEVICE otherwise); a wait that still runs past its bound
+ * (other work holding CUs) sets FLEET_MOE_ABORT_UNIT_WAIT or _ROUTER_WAIT. */
 int fleet_moe_layer_decode(const fleet_moe_layer* layer, const float* x, float* x_out,
                            uint16_t* moe_out, int32_t* ids, float* weights,
                            void* workspace, size_t workspace_bytes,
@@ -128,10 +132,12 @@ size_t fleet_moe_grouped_workspace_bytes(const fleet_moe_dims* dims, int32_t max
  * order. One launch over every CU (256 workgroups resident at once) for
  * n_tokens <= 8, two (gate/up, then down + combine) above that.
  * x_norm: bf16[n_tokens][hidden]; ids: int32[n_tokens][top_k] (each in
- * [0, n_routed), distinct per token); weights: fp32[n_tokens][top_k];
+ * [0, n_routed), distinct per token; an id outside that range is clamped into
+ * it and raises FLEET_MOE_ABORT_BAD_ID); weights: fp32[n_tokens][top_k];
  * out: bf16[n_tokens][hidden]. 1 <= n_tokens <= max_tokens of the workspace
- * (max_tokens <= 256). Workspace words carry a 32-bit call count: a
- * workspace is good for 2^32 calls. */
+ * (max_tokens <= 256). Workspace words carry a 32-bit call count; the call
+ * numbered 2^32 - 1 clears them and restarts the count, so a workspace never
+ * needs to be zero-filled again. */
 int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens, const int32_t* ids,
                       const float* weights, const uint16_t* x_norm, uint16_t* out,
                       void* workspace, size_t workspace_bytes, const fleet_moe_dims* dims,
@@ -220,6 +226,8 @@ int fleet_moe_workspace_status(const void* workspace, uint32_t* status, hipStrea
 #define FLEET_MOE_ABORT_POSITION 0x8u     /* device position outside [0, max_pos) */
 #define FLEET_MOE_ABORT_TOKEN 0x10u       /* device token outside the vocabulary */
 #define FLEET_MOE_ABORT_ATTN_WAIT 0x20u   /* an attention stage never completed */
+#define FLEET_MOE_ABORT_BAD_ID 0x40u      /* grouped: an expert id outside [0, n_routed)
+                                             was clamped into range (output unspecified) */
 
 /* Diagnostic: reads `bytes` of device memory with the weight-streaming load
  * pattern of the kernels above (16-byte non-temporal loads, 1 KB per wave

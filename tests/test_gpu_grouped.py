@@ -141,3 +141,57 @@ def test_grouped_workspace_reuse_across_token_counts(dev):
         want = orc.moe_grouped(pl, xn, ids, ws)["out"]
         assert rel_err(got, want) <= 1e-2, f"call {n} T={T}"
     assert runner.status() == 0
+
+
+def test_grouped_out_of_range_ids_raise_the_status_bit(dev):
+    """An id outside [0, 64) is clamped (the addresses stay in bounds) and
+    reported through FLEET_MOE_ABORT_BAD_ID; a valid call reports nothing."""
+    layer, pl = dev
+    from fleet_moe import _lib
+    T = 4
+    xn = orc.rms_norm(synth.hidden_inputs(90, T))
+    _, ids, ws = orc.route(pl.router_f32(), xn)
+    x = torch.from_numpy(orc.bf16_bits(xn).view(np.int16)).cuda()
+    runner = ops.GroupedRunner(T, DSV2_LITE)
+    say("grouped valid ids")
+    runner.run(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(ws).cuda())
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    bad = ids.copy()
+    bad[2, 3] = 64
+    bad[0, 0] = -1
+    say("grouped ids out of range")
+    runner.run(layer, x, torch.from_numpy(bad).cuda(), torch.from_numpy(ws).cuda())
+    torch.cuda.synchronize()
+    assert runner.status() == _lib.ABORT_BAD_ID
+
+
+def test_grouped_call_count_wrap_restarts_a_clean_workspace(dev):
+    """Workspace words carry a 32-bit call count. The header is seeded from the
+    host as if 2^32 - 3 calls had run; the call numbered 2^32 - 1 clears the
+    tagged words and restarts the count at 0, so the calls on either side of
+    the wrap give the same outputs as a fresh workspace, bit for bit."""
+    layer, pl = dev
+    T_max = 64
+    runner = ops.GroupedRunner(T_max, DSV2_LITE)
+    fresh = ops.GroupedRunner(T_max, DSV2_LITE)
+    start = 0xFFFFFFFD          # header words: call count, exit count (256 per call)
+    head0 = np.array([start, (start * 256) & 0xFFFFFFFF], np.uint32)
+    runner.workspace[:8].copy_(torch.from_numpy(head0.view(np.uint8)).cuda())
+    bias = synth.zipf_logit_bias(3)
+    for n, T in enumerate((16, 4, 64, 9, 4)):
+        xn = orc.rms_norm(synth.hidden_inputs(110 + n, T))
+        _, ids, ws = orc.route(pl.router_f32(), xn, logit_bias=bias)
+        x = torch.from_numpy(orc.bf16_bits(xn).view(np.int16)).cuda()
+        idt, wst = torch.from_numpy(ids).cuda(), torch.from_numpy(ws).cuda()
+        say(f"grouped wrap call {n} (count {(start + 1 + n) & 0xFFFFFFFF:#x}) T={T}")
+        got = runner.run(layer, x, idt, wst)
+        want = fresh.run(layer, x, idt, wst)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {n} T={T}"
+        head = runner.workspace[:8].cpu().numpy().view(np.uint32).tolist()
+        if n == 0:
+            assert head == [start + 1, ((start + 1) * 256) & 0xFFFFFFFF]
+        else:           # the call numbered 2^32 - 1 (n = 1) restarted the count at 0
+            assert head == [n - 1, 256 * (n - 1)]
+    assert runner.status() == 0
