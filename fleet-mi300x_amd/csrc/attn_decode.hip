@@ -100,7 +100,9 @@ struct Workspace {
     // Published values. Every 32-bit word is (epoch & 0xffff) << 16 | 16
     // payload bits: a bf16 in one word, an fp32 in two (high half first), an
     // fp64 in four, so a word read with any tearing of wider accesses still
-    // proves its own freshness.
+    // proves its own freshness. Every call rewrites every one of these words
+    // (chunks without positions publish neutral partials), so a 16-bit tag
+    // only has to differ from the previous call's.
     uint32_t qkv_t[kQkvRows];                  // bf16 q / kv_a
     uint32_t qc_t[kHeads][kLora][2];           // fp32 q_c
     uint32_t ml_t[kHeads][kChunks][8];         // fp64 chunk max, then fp64 chunk sum of exp
@@ -781,6 +783,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         if (tid == 0) {
             publish_f64(&ws->ml_t[h][k][0], M, tag);
             publish_f64(&ws->ml_t[h][k][4], Ls, tag);
+        }
+    } else {
+        // A chunk without positions (pos < 15) still publishes, a neutral
+        // partial (max -inf, sums 0) that no merge reads: every polled word
+        // is then rewritten on every call, so a word is never older than one
+        // call and its 16-bit tag can never equal the current one by wrapping.
+        publish_f64(ws->o_t[h][k][tid], 0.0, tag);
+        if (tid == 0) {
+            publish_f64(&ws->ml_t[h][k][0], -INFINITY, tag);
+            publish_f64(&ws->ml_t[h][k][4], 0.0, tag);
         }
     }
     ATTN_TRACE(9);

@@ -176,6 +176,46 @@ def test_attention_in_place_and_device_position_and_graph(attn_setup):
     assert dec.status() == 0
 
 
+def test_attention_tags_cannot_alias_after_65536_calls(attn_setup):
+    """Published words carry the low 16 bits of the call count. A call at a
+    short position leaves chunks without positions; those chunks must still
+    publish (neutral partials), or a later call whose 16-bit tag equals the
+    one their stale words carry could merge them. The workspace's call count
+    is set from the host to stand in for 65,535 intervening calls, so call C
+    has call A's tag; A and C attend with different inputs (so A's partials
+    differ from C's), and C must still equal the oracle bit for bit."""
+    S = attn_setup
+    w, rng, cos, sin = S["w"], S["rng"], S["cos"], S["sin"]
+    host_cache = S["cache"].copy()
+    cache_d = dev16(bits(host_cache))
+    dec = ops.AttnDecoder(DSV2_LITE)
+    pos_long, pos_short = 1055, 3
+
+    def call(x, pos):
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty_like(xd)
+        dec.attn_into(S["layer"], xd, yd, cache_d, pos, None, S["cos_d"], S["sin_d"])
+        torch.cuda.synchronize()
+        assert dec.status() == 0
+        host_cache[pos] = orc.bf16_to_f32(cache_d[pos].cpu().numpy().view(np.uint16))
+        return yd.cpu().numpy()
+
+    say("tag wrap: call A at 1055, call B at 3")
+    call(_x(rng), pos_long)                     # call 1: every chunk's words get tag 1
+    call(_x(rng), pos_short)                    # call 2: chunks 4..15 hold no positions
+    head = np.array([65536, (65536 * 256) & 0xFFFFFFFF], np.uint32)   # call count, exits
+    dec.workspace[:8].copy_(torch.from_numpy(head.view(np.uint8)).cuda())
+    say("tag wrap: call C at 1055 with call A's tag")
+    x = _x(rng)
+    want_cache = host_cache.copy()
+    got = call(x, pos_long)                     # call 65537: tag 1 again
+    r = orc.attention(w, x, want_cache, pos_long, cos, sin)
+    want = orc.bf16_round(x + r["out"])
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32),
+                                  err_msg="call with a wrapped tag")
+    assert dec.workspace[:4].view(torch.int32).item() == 65537
+
+
 def test_attention_position_checks(attn_setup):
     S = attn_setup
     dec = ops.AttnDecoder(DSV2_LITE)
