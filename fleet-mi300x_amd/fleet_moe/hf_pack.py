@@ -169,10 +169,12 @@ def pack_checkpoint(model_dir, out, log=print) -> dict:
             gu = interleave_gate_up(m("gate_proj.weight"), m("up_proj.weight"))
             w.write(f"L{i}.dense", np.concatenate([gu.reshape(-1),
                                                    m("down_proj.weight").reshape(-1)]))
-        log(f"  layer {i:2d} packed, {w.pos / 1e9:.2f} GB")
+        log(f"hf_pack: L{i} done ({'moe' if f'L{i}.router' in w.offsets else 'dense'}), "
+            f"blob at {w.pos:,} bytes")
     w.close()
     if len(set(expert_strides)) > 1:
-        raise ValueError(f"expert stride differs across layers: {set(expert_strides)}")
+        raise ValueError(f"MoE layers disagree on the routed-expert block size "
+                         f"(elements): {sorted(set(expert_strides))}")
 
     rs = cfg.get("rope_scaling") or {}
     meta = {
@@ -208,7 +210,8 @@ def pack_checkpoint(model_dir, out, log=print) -> dict:
     }
     Path(str(out) + ".json").write_text(json.dumps(meta, indent=2))
     write_manifest(Path(str(out) + ".manifest"), meta)
-    log(f"wrote {out} ({w.pos / 1e9:.2f} GB), {out}.json and {out}.manifest")
+    log(f"hf_pack: {w.pos:,} bytes of bf16 in {out}; metadata in {out}.json, "
+        f"manifest in {out}.manifest")
     return meta
 
 
