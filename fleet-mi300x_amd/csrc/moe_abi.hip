@@ -153,6 +153,22 @@ __global__ __launch_bounds__(kThreads) void router_topk_kernel(Params P) {
 
 }  // namespace router
 
+namespace fold {
+
+// x_out = bf16(x + bf16(p_0 + p_1 + ... + p_{n-1})), the partials added in
+// fp32 in index order (one thread per hidden element; x may equal x_out).
+constexpr int kThreads = 256;
+__global__ __launch_bounds__(kThreads) void residual_fold_kernel(const float* x,
+                                                                 const float* partials,
+                                                                 int n_partials, float* x_out) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    float acc = partials[i];
+    for (int p = 1; p < n_partials; ++p) acc += partials[(int64_t)p * kHidden + i];
+    x_out[i] = bf16r(x[i] + bf16r(acc));
+}
+
+}  // namespace fold
+
 namespace probe {
 
 // Streaming read with the weight-load pattern of the MoE kernels: each wave
@@ -213,6 +229,19 @@ extern "C" int fleet_moe_router_topk(const uint16_t* w_router, const float* x_no
     P.scaling = dims->routed_scaling;
     hipLaunchKernelGGL(router::router_topk_kernel, dim3(n_tokens), dim3(router::kThreads), 0,
                        stream, P);
+    return (int)hipGetLastError();
+}
+
+extern "C" int fleet_moe_residual_fold(const float* x, const float* partials, int32_t n_partials,
+                                       float* x_out, const fleet_moe_dims* dims,
+                                       hipStream_t stream) {
+    if (int e = check_dims_impl(dims)) return e;
+    if (!x || !partials || !x_out || n_partials < 1 || n_partials > 64 || !aligned(x, 4) ||
+        !aligned(partials, 4) || !aligned(x_out, 4))
+        return FLEET_MOE_ERR_ARG;
+    if (int e = check_device_impl(1)) return e;
+    hipLaunchKernelGGL(fold::residual_fold_kernel, dim3(kHidden / fold::kThreads),
+                       dim3(fold::kThreads), 0, stream, x, partials, n_partials, x_out);
     return (int)hipGetLastError();
 }
 

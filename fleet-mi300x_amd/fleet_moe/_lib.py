@@ -49,6 +49,8 @@ SYMBOLS = [
     ("fleet_moe_router_topk", c_int,
      [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
       POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_moe_residual_fold", c_int,
+     [c_void_p, c_void_p, c_int32, c_void_p, POINTER(FleetMoeDims), c_void_p]),
     ("fleet_moe_layer_workspace_bytes", c_size_t, [POINTER(FleetMoeDims)]),
     ("fleet_moe_layer_decode", c_int,
      [POINTER(FleetMoeLayer), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

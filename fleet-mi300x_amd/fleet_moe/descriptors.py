@@ -14,14 +14,32 @@ and the consumer of that event (the next layer's first tasks, or LM_HEAD)
 carries FOLD_PARTIALS: its prologue adds the eight expert partials to the
 residual stream.
 
+The residual stream is two buffers (fleet_types.h Activations.x): x[0], the
+layer input, and x[1], the residual after attention. The NORM_ROUTER prologue
+forms x[1] = bf16(x[0] + bf16(sum of o_proj's eight fp32 partials))
+(fleet_kernel.hip:405-425), unless o_proj splits rows (OPROJ_ROW_SPLIT) and
+writes x[1] itself. With --local-fold (taskgraph.py:752-829) the folds move
+into REDUCE tasks, one per XCD: head 0 forms x[1] for the NORM_ROUTER tasks,
+head 1 adds an MoE layer's expert partials for the next QKV_FUSED / LM_HEAD
+tasks, which then read the REDUCE's per-XCD copy (LOCAL_FOLD).
+
 `plan()` reads such a list (and the `.events.txt` sidecar, when given) and cuts
-it into graph segments around every MoE layer: each MoE layer becomes one
-`fleet_moe_layer_decode` call, which does the norm, routing, experts, combine
-and residual add in one launch. Waits on events produced before a cut are
-satisfied by stream order and cleared, and FOLD_PARTIALS is cleared on the
-consumers (the residual is already final). Every MoE layer must be complete
-(a router task on every XCD, gate_up and down for every routed slot and both
-shared halves) or `plan()` raises.
+it into graph segments around every MoE layer. Each MoE layer becomes one
+`MoeCall`: `fleet_moe_residual_fold` (x[0] + o_proj partials -> x[1]) when
+the layer's o_proj is K-split, then `fleet_moe_layer_decode` in place on
+x[1], which does the norm, routing, experts, combine and residual add, so
+x[1] leaves the call as the next layer's input and no expert partials exist.
+Accordingly:
+  * the layer's head-0 REDUCE tasks are absorbed into its call (the call
+    folds o_proj's partials itself);
+  * head-1 REDUCE tasks that fold its expert partials are dropped, and their
+    consumers lose LOCAL_FOLD and FOLD_PARTIALS and read x[1];
+  * waits on events produced before a cut are satisfied by stream order and
+    cleared; FOLD_PARTIALS is cleared on the consumers of the layer's done
+    event.
+Every MoE layer must be complete (a router task on every XCD, gate_up and down
+for every routed slot and both shared halves), and no task outside the layer
+may wait on one of its internal events, or `plan()` raises `PlanError`.
 
 `MoeSteps.run()` executes the MoE calls of a plan on this library; the graph
 segments are left to the runtime that owns them.
@@ -184,6 +202,10 @@ class MoeLayer:
         _ = self.done_event
 
 
+class PlanError(ValueError):
+    """A task graph that cannot be mapped onto the library's MoE calls."""
+
+
 @dataclass
 class Segment:
     """Graph descriptors to run as one launch of the owning runtime."""
@@ -192,9 +214,13 @@ class Segment:
 
 @dataclass
 class MoeCall:
-    """One fleet_moe_layer_decode call replacing a MoE layer's tasks."""
+    """One MoE layer replaced by library calls: the o_proj fold into x[1]
+    (when `fold_oproj`), then fleet_moe_layer_decode in place on x[1].
+    `absorbed` lists the graph's REDUCE tasks the call replaces."""
     layer: int
     source: MoeLayer
+    fold_oproj: bool = True
+    absorbed: list[Descriptor] = field(default_factory=list)
 
 
 def _moe_layers(descs: list[Descriptor]) -> dict[int, MoeLayer]:
@@ -210,6 +236,17 @@ def _moe_layers(descs: list[Descriptor]) -> dict[int, MoeLayer]:
     return out
 
 
+def _internal_events(m: MoeLayer) -> set[int]:
+    """Events a MoE layer's tasks signal or use locally, except its done event."""
+    ev = set()
+    for d in m.routers + m.gate_up + m.down:
+        for e in (d.signal_event, d.local_event):
+            if e >= 0:
+                ev.add(e)
+    ev.discard(m.done_event)
+    return ev
+
+
 def plan(descs: list[Descriptor], top_k: int = 6, events: list[Event] | None = None,
          n_xcds: int = N_XCDS) -> list[Segment | MoeCall]:
     """Cut a descriptor list into runtime segments and MoE calls, in order.
@@ -222,11 +259,52 @@ def plan(descs: list[Descriptor], top_k: int = 6, events: list[Event] | None = N
         for d in descs:
             for ev in (d.wait_event, d.signal_event):
                 if ev >= 0 and ev not in ids:
-                    raise ValueError(f"descriptor {d.index}: event {ev} not in the event table")
+                    raise PlanError(f"descriptor {d.index}: event {ev} not in the event table")
     layers = _moe_layers(descs)
     for m in layers.values():
         m.check(top_k, n_xcds)
     done = {m.done_event: m.layer for m in layers.values()}
+    internal = {e: m.layer for m in layers.values() for e in _internal_events(m)}
+    waiters: dict[int, list[Descriptor]] = {}
+    for d in descs:
+        if d.wait_event >= 0:
+            waiters.setdefault(d.wait_event, []).append(d)
+
+    calls: dict[int, MoeCall] = {}
+    for L, m in layers.items():
+        split = {bool(d.flags & Flags.OPROJ_ROW_SPLIT) for d in m.routers}
+        if len(split) != 1:
+            raise PlanError(f"layer {L}: NORM_ROUTER tasks disagree on OPROJ_ROW_SPLIT")
+        calls[L] = MoeCall(L, m, fold_oproj=not split.pop())
+
+    # --local-fold publishers: head 0 before an MoE layer's routers (absorbed),
+    # head 1 after it (dropped; its readers read x[1] instead)
+    absorbed: set[int] = set()          # id() of REDUCE descriptors taken out
+    retired: dict[int, int] = {}        # head-1 publication event -> MoE layer
+    for d in descs:
+        if d.kind != TaskKind.REDUCE or not d.flags & Flags.LOCAL_FOLD:
+            continue
+        readers = waiters.get(d.signal_event, [])
+        if d.head == 0 and d.layer in layers:
+            bad = [r for r in readers if not (r.kind == TaskKind.NORM_ROUTER and r.layer == d.layer)]
+            if bad:
+                raise PlanError(f"REDUCE {d.index} (o_proj fold of MoE layer {d.layer}) is read "
+                                f"by tasks other than the layer's routers: {[r.index for r in bad]}")
+            calls[d.layer].absorbed.append(d)
+            absorbed.add(id(d))
+        elif d.head == 1 and d.wait_event in done:
+            L = done[d.wait_event]
+            bad = [r for r in readers if r.kind not in (TaskKind.QKV_FUSED, TaskKind.LM_HEAD)]
+            if bad:
+                raise PlanError(f"REDUCE {d.index} (expert fold of MoE layer {L}) is read by "
+                                f"unexpected tasks {[r.index for r in bad]}")
+            calls[L].absorbed.append(d)
+            absorbed.add(id(d))
+            retired[d.signal_event] = L
+        elif d.wait_event in done or d.wait_event in internal:
+            raise PlanError(f"REDUCE {d.index} (head {d.head}) waits on MoE layer "
+                            f"{done.get(d.wait_event, internal.get(d.wait_event))}, "
+                            "which this library replaces; its fold cannot be mapped")
 
     steps: list[Segment | MoeCall] = []
     produced_before: set[int] = set()     # events signalled by earlier steps
@@ -245,18 +323,29 @@ def plan(descs: list[Descriptor], top_k: int = 6, events: list[Event] | None = N
         if d.layer in layers and d.kind in MOE_KINDS:
             if d.layer not in emitted:
                 close_segment()
-                steps.append(MoeCall(d.layer, layers[d.layer]))
+                steps.append(calls[d.layer])
                 emitted.add(d.layer)
-                produced_before.update({t.signal_event for t in
-                                        layers[d.layer].routers + layers[d.layer].gate_up +
-                                        layers[d.layer].down if t.signal_event >= 0})
+                m = layers[d.layer]
+                produced_before.update({t.signal_event for t in m.routers + m.gate_up + m.down
+                                        if t.signal_event >= 0})
+                produced_before.update({t.signal_event for t in calls[d.layer].absorbed})
             continue
+        if id(d) in absorbed:
+            continue
+        if d.wait_event in internal:
+            raise PlanError(f"descriptor {d.index} ({TaskKind(d.kind).name}) waits on an "
+                            f"internal event of MoE layer {internal[d.wait_event]}")
         nd = d
+        if d.wait_event in retired:
+            L = retired[d.wait_event]
+            if L not in emitted:
+                raise PlanError(f"descriptor {d.index} reads MoE layer {L}'s fold before the layer")
+            nd = replace(nd, flags=int(Flags(nd.flags) & ~(Flags.LOCAL_FOLD | Flags.FOLD_PARTIALS)))
+        if d.wait_event in done:
+            nd = replace(nd, flags=int(Flags(nd.flags) & ~Flags.FOLD_PARTIALS))
         if nd.wait_event >= 0 and nd.wait_event in produced_before:
             # satisfied by stream order: the producer ran in an earlier step
             nd = replace(nd, wait_event=-1, wait_scope=0, wait_count=0)
-        if d.wait_event in done and d.flags & Flags.FOLD_PARTIALS:
-            nd = replace(nd, flags=int(Flags(nd.flags) & ~Flags.FOLD_PARTIALS))
         cur.append(replace(nd, index=len(cur)))
         if d.signal_event >= 0:
             seg_events.add(d.signal_event)
@@ -265,26 +354,40 @@ def plan(descs: list[Descriptor], top_k: int = 6, events: list[Event] | None = N
 
 
 class MoeSteps:
-    """Runs the MoE calls of a plan through fleet_moe_layer_decode.
+    """Runs the MoE calls of a plan: fleet_moe_residual_fold (for a call with
+    `fold_oproj`), then fleet_moe_layer_decode in place on x[1].
 
     `layers` maps a graph layer index to a `DeviceLayer`; one decoder (and its
-    workspace) serves all of them, in order, on one stream."""
+    workspace) serves all of them, in order, on one stream. `fold` is
+    `ops.residual_fold` unless given."""
 
-    def __init__(self, steps: list[Segment | MoeCall], layers: dict, decoder):
+    def __init__(self, steps: list[Segment | MoeCall], layers: dict, decoder, fold=None):
         self.steps = steps
         self.layers = layers
         self.decoder = decoder
+        if fold is None:
+            from .ops import residual_fold as fold
+        self.fold = fold
         missing = [s.layer for s in steps if isinstance(s, MoeCall) and s.layer not in layers]
         if missing:
             raise KeyError(f"no weights for MoE layers {missing}")
 
-    def run(self, x, segment_runner=None, stream=None) -> None:
-        """x: fp32[hidden] residual stream on the device, updated in place.
+    def run(self, x_in, x_mid, oproj_partials=None, segment_runner=None, stream=None) -> None:
+        """The runtime's residual buffers, fp32 device tensors: x_in = x[0]
+        (the layer input), x_mid = x[1] (the residual after attention; each
+        MoE call leaves the next layer's input there), oproj_partials = o_proj's
+        K-split partials [n][hidden] (read by calls with `fold_oproj`).
         `segment_runner(segment)` runs the non-MoE descriptors (the owning
-        runtime); without one, only MoE calls may appear in the plan."""
+        runtime, which fills those buffers); without one, only MoE calls may
+        appear in the plan. Nothing is allocated."""
         for s in self.steps:
             if isinstance(s, MoeCall):
-                self.decoder.decode_into(self.layers[s.layer], x, x, stream=stream)
+                if s.fold_oproj:
+                    if oproj_partials is None:
+                        raise ValueError(f"MoE layer {s.layer} folds o_proj's partials: "
+                                         "pass oproj_partials")
+                    self.fold(x_in, oproj_partials, x_mid, self.decoder.dims, stream)
+                self.decoder.decode_into(self.layers[s.layer], x_mid, x_mid, stream=stream)
             elif segment_runner is not None:
                 segment_runner(s)
             else:
@@ -292,7 +395,8 @@ class MoeSteps:
 
 
 def moe_layer_descriptors(layer: int, wait_event: int, first_event: int, top_k: int = 6,
-                          n_xcds: int = N_XCDS, workers: int = 37) -> tuple[list[Descriptor], int]:
+                          n_xcds: int = N_XCDS, workers: int = 37,
+                          oproj_row_split: bool = False) -> tuple[list[Descriptor], int]:
     """Descriptors of one MoE layer in the reference's shape (a router task per
     XCD, then gate_up and down per XCD with slot = xcd for xcd < top_k, else a
     shared half -1, -2), with fresh event ids from `first_event`. Returns the
@@ -304,7 +408,8 @@ def moe_layer_descriptors(layer: int, wait_event: int, first_event: int, top_k: 
     for x in range(n_xcds):
         out.append(Descriptor(TaskKind.NORM_ROUTER, layer, x, wait_event=wait_event,
                               signal_event=ev, signal_scope=Scope.XCD_LOCAL,
-                              n_split=workers))
+                              n_split=workers,
+                              flags=Flags.OPROJ_ROW_SPLIT if oproj_row_split else Flags.NONE))
         routed.append(ev)
         ev += 1
     chunk = []
@@ -335,5 +440,5 @@ def field_offsets() -> dict[str, int]:
 
 
 __all__ = ["DESCRIPTOR_BYTES", "FIELD_NAMES", "TaskKind", "Flags", "Scope", "Descriptor",
-           "Event", "MoeLayer", "Segment", "MoeCall", "MoeSteps", "pack_all", "unpack_all",
+           "Event", "MoeLayer", "PlanError", "Segment", "MoeCall", "MoeSteps", "pack_all", "unpack_all",
            "parse_events", "plan", "moe_layer_descriptors", "field_offsets"]

@@ -92,6 +92,17 @@ def route(layer: DeviceLayer, x_norm: torch.Tensor, logit_bias: torch.Tensor | N
     return logits, ids, ws
 
 
+def residual_fold(x: torch.Tensor, partials: torch.Tensor, x_out: torch.Tensor,
+                  dims: MoeDims = DSV2_LITE, stream=None) -> None:
+    """x_out = bf16(x + bf16(sum of partials in index order)): the residual
+    after attention from the layer input and o_proj's K-split fp32 partials
+    [n][hidden] (the NORM_ROUTER prologue's fold). Enqueued, no allocation."""
+    cd = c_dims(dims)
+    rc = _lib.load().fleet_moe_residual_fold(_ptr(x), _ptr(partials), int(partials.shape[0]),
+                                             _ptr(x_out), ctypes.byref(cd), _stream(stream))
+    _lib.check(rc, "fleet_moe_residual_fold")
+
+
 class LayerDecoder:
     """Batch-1 MoE layer decode with its own persistent workspace.
 

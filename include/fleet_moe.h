@@ -78,6 +78,17 @@ int fleet_moe_router_topk(const uint16_t* router, const float* x_norm, int32_t n
                           const float* logit_bias, float* logits, int32_t* ids,
                           float* weights, const fleet_moe_dims* dims, hipStream_t stream);
 
+/* The residual fold of the NORM_ROUTER prologue (stage_residual_f32,
+ * src/kernels/fleet_kernel.hip:107-144, called at :405-425): the post-
+ * attention residual x[1] = bf16(x[0] + bf16(p_0 + ... + p_{n-1})) from the
+ * layer input and o_proj's n K-split fp32 partials (Activations.oproj_partial,
+ * [n][hidden], n = 8 in the reference), the partials added in fp32 in index
+ * order. fleet_moe_layer_decode takes that x[1] as its input; a graph whose
+ * o_proj writes x[1] itself (OPROJ_ROW_SPLIT) needs no fold.
+ * x, x_out: fp32[hidden] (may be equal); 1 <= n_partials <= 64. */
+int fleet_moe_residual_fold(const float* x, const float* partials, int32_t n_partials,
+                            float* x_out, const fleet_moe_dims* dims, hipStream_t stream);
+
 /* Workspace bytes fleet_moe_layer_decode needs. */
 size_t fleet_moe_layer_workspace_bytes(const fleet_moe_dims* dims);
 

@@ -79,6 +79,21 @@ def bf16_to_f32(bits) -> np.ndarray:
     return (b.astype(np.uint32) << np.uint32(16)).view(np.float32)
 
 
+# ---------------------------------------------------------------- a1 residual fold
+
+def residual_fold(x, partials) -> np.ndarray:
+    """The post-attention residual x[1] = bf16(x[0] + bf16(sum of o_proj's
+    K-split fp32 partials)), the partials added in fp32 one after the other in
+    index order (the non-coherent path of stage_residual_f32,
+    src/kernels/fleet_kernel.hip:107-144: acc = p[0]; acc += p[x] for x = 1..7;
+    then the two roundings). x: fp32 [H]; partials: fp32 [n][H]."""
+    p = np.asarray(partials, np.float32)
+    acc = p[0].copy()
+    for q in p[1:]:
+        acc = (acc + q).astype(np.float32)
+    return bf16_round(np.asarray(x, np.float32) + bf16_round(acc))
+
+
 # ---------------------------------------------------------------- a1 RMSNorm
 
 def rms_norm(x, gamma=None, eps: float = RMS_EPS) -> np.ndarray:

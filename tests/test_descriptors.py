@@ -145,10 +145,25 @@ def test_moe_steps_need_weights_and_a_segment_runner():
         def decode_into(self, layer, x, x_out, stream=None):
             calls.append((layer, x is x_out))
 
-    ms = D.MoeSteps(steps, {1: "w1", 2: "w2"}, Dec())
+    Dec.dims = None
+    folds = []
+    ms = D.MoeSteps(steps, {1: "w1", 2: "w2"}, Dec(),
+                    fold=lambda x, p, out, dims, stream: folds.append((x, p, out)))
     with pytest.raises(RuntimeError):
-        ms.run("x")
+        ms.run("x0", "x1", "p")
+    with pytest.raises(ValueError, match="oproj_partials"):
+        ms.run("x0", "x1", None, segment_runner=lambda s: None)
     segs = []
     calls.clear()
-    ms.run("x", segment_runner=segs.append)
+    folds.clear()
+    ms.run("x0", "x1", "p", segment_runner=segs.append)
+    # each call: x[1] = fold(x[0], partials), then the layer in place on x[1]
+    assert folds == [("x0", "p", "x1")] * 2
     assert calls == [("w1", True), ("w2", True)] and len(segs) == 3
+    # o_proj row-split graphs write x[1] themselves: no fold
+    g2 = [D.replace(d, flags=d.flags | D.Flags.OPROJ_ROW_SPLIT)
+          if d.kind == D.TaskKind.NORM_ROUTER and d.layer > 0 else d for d in g]
+    folds.clear()
+    D.MoeSteps(D.plan(g2), {1: "w1", 2: "w2"}, Dec(),
+               fold=lambda *a: folds.append(a)).run("x0", "x1", segment_runner=segs.append)
+    assert folds == []

@@ -79,6 +79,35 @@ def hf_rmsnorm_bf16(x: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
     return (t_bf16(gamma) * h.to(torch.bfloat16)).to(torch.float32).numpy()
 
 
+def test_residual_fold_order_and_roundings():
+    """residual_fold = bf16(x + bf16(p_0 + ... + p_7)), fp32 adds in index
+    order (stage_residual_f32, fleet_kernel.hip:107-144). Planted cases, each
+    failing one plausible mistake."""
+    z = np.zeros(2048, np.float32)
+
+    def fold1(x0, ps):
+        parts = np.zeros((8, 2048), np.float32)
+        for i, v in enumerate(ps):
+            parts[i, 0] = v
+        x = z.copy()
+        x[0] = x0
+        return float(orc.residual_fold(x, parts)[0])
+    # index order: 1e8 + 1 rounds to 1e8 in fp32, so the 1 survives only after
+    # the cancellation (a pairwise or reversed order gives 0 here)
+    assert fold1(0.0, [1e8, 1.0, -1e8, 1.0]) == 1.0
+    assert fold1(0.0, [1.0, 1e8, -1e8]) == 0.0
+    # the inner bf16 rounding: bf16(2^-8 + 2^-16) = 2^-8, then 1 + 2^-8 is a
+    # tie that rounds to even (1.0); without it the sum rounds up
+    assert fold1(1.0, [2.0 ** -8 + 2.0 ** -16]) == 1.0
+    # the outer rounding: 1 + 2^-10 is not a bf16 value
+    assert fold1(1.0, [2.0 ** -10]) == 1.0
+    # exactly representable values: the fold is the plain sum
+    rng = np.random.default_rng(0)
+    x = rng.integers(-64, 64, 2048).astype(np.float32)
+    parts = rng.integers(-16, 16, (8, 2048)).astype(np.float32)
+    np.testing.assert_array_equal(orc.residual_fold(x, parts), x + parts.sum(0))
+
+
 def test_rms_norm_matches_torch_hf_module():
     rng = np.random.default_rng(1)
     x = rng.standard_normal((64, 2048)).astype(np.float32)
