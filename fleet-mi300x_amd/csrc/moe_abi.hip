@@ -278,6 +278,12 @@ extern "C" const char* fleet_moe_error_string(int code) {
         case FLEET_MOE_ERR_DEVICE:
             return "fleet_moe: device is not a gfx950 with enough CUs to hold one workgroup of "
                    "the kernel on each";
+        case FLEET_MOE_ERR_CAPACITY:
+            return "fleet_moe: more tokens than the static scratch of the no-allocation entry "
+                   "point holds";
+        case FLEET_MOE_ERR_CAPTURE:
+            return "fleet_moe: the first no-allocation call on a device sets up its scratch and "
+                   "must not be made under graph capture";
         default: return hipGetErrorString((hipError_t)code);
     }
 }

@@ -38,6 +38,9 @@
 // records FLEET_MOE_ABORT_GROUP_WAIT instead of hanging.
 #include <stddef.h>
 
+#include <mutex>
+#include <vector>
+
 #include "moe_common.h"
 
 namespace fleet_moe {
@@ -1226,3 +1229,89 @@ extern "C" int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens,
                           static_cast<char*>(workspace), max_tokens, stream);
 }
 
+// ------------------------------------------------- the variant that allocates nothing
+//
+// fleet_moe_grouped_noalloc runs the same kernels on `scratch`, a file-scope
+// device array laid out exactly like a caller workspace sized for
+// kScratchTokens tokens. Each device holds its own copy at its own address;
+// host code never passes the array's name to a kernel (on the host it is only
+// a stand-in for the symbol), only the per-device address that
+// hipGetSymbolAddress returns at the first call on that device.
+namespace fleet_moe {
+namespace grouped {
+
+constexpr int kScratchTokens = 64;
+constexpr size_t kScratchBytes = layout(kScratchTokens).total;   // 7,574,528 B
+
+__global__ __launch_bounds__(256) void scratch_clear_kernel(u32x4* p, size_t n16) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n16; i += gridDim.x * (size_t)256)
+        p[i] = z;
+}
+
+// Reads and clears the step's status word (ordered after the step's kernels
+// on the stream, so it sees every bit they raised).
+__global__ void status_take_kernel(Header* hdr, uint32_t* status) {
+    if (threadIdx.x == 0)
+        status[0] = __hip_atomic_exchange(&hdr->abort, 0u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace grouped
+}  // namespace fleet_moe
+
+static __device__ __align__(256) uint8_t scratch[grouped::kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<char*> g_scratch;   // per device: the address of `scratch`, once set up
+}  // namespace
+
+// The calling thread's current device's copy of `scratch`. At the first call on
+// a device: look up its address and zero it (a fill kernel on `stream`, then a
+// synchronize, so later calls on any stream see it cleared). That first call
+// must not be under graph capture.
+static int scratch_of_current_device(hipStream_t stream, char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1, nullptr);
+    if (!g_scratch[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return (int)e;
+        if (cs != hipStreamCaptureStatusNone) return FLEET_MOE_ERR_CAPTURE;
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p || !aligned(p, 256)) return FLEET_MOE_ERR_DEVICE;
+        hipLaunchKernelGGL(grouped::scratch_clear_kernel, dim3(1024), dim3(256), 0, stream,
+                           static_cast<u32x4*>(p), grouped::kScratchBytes / 16);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return (int)e;
+        g_scratch[dev] = static_cast<char*>(p);
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+
+extern "C" int fleet_moe_grouped_noalloc(const fleet_moe_layer* layer, int32_t n_tokens,
+                                         const int32_t* ids, const float* weights,
+                                         const uint16_t* x_norm, uint16_t* out,
+                                         uint32_t* status, const fleet_moe_dims* dims,
+                                         hipStream_t stream) {
+    if (int e = check_grouped_args(layer, n_tokens, ids, weights, x_norm, out, dims)) return e;
+    if (!status || !aligned(status, 4)) return FLEET_MOE_ERR_ARG;
+    if (n_tokens > grouped::kScratchTokens) return FLEET_MOE_ERR_CAPACITY;
+    if (int e = check_grouped_resident()) return e;
+    char* ws = nullptr;
+    if (int e = scratch_of_current_device(stream, &ws)) return e;
+    if (int e = launch_grouped(layer, n_tokens, ids, weights, x_norm, out, ws,
+                               grouped::kScratchTokens, stream))
+        return e;
+    hipLaunchKernelGGL(grouped::status_take_kernel, dim3(1), dim3(64), 0, stream,
+                       reinterpret_cast<grouped::Header*>(ws), status);
+    return (int)hipGetLastError();
+}

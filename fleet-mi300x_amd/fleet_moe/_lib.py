@@ -15,6 +15,11 @@ ERR_DIMS = 10001
 ERR_ARG = 10002
 ERR_WORKSPACE = 10003
 ERR_DEVICE = 10004
+ERR_CAPACITY = 10005
+ERR_CAPTURE = 10006
+
+NOALLOC_MAX_TOKENS = 64
+NOALLOC_SCRATCH_BYTES = 7574528
 
 ABORT_ROUTER_WAIT = 0x1
 ABORT_UNIT_WAIT = 0x2
@@ -63,6 +68,9 @@ SYMBOLS = [
     ("fleet_moe_grouped", c_int,
      [POINTER(FleetMoeLayer), c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
       c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_moe_grouped_noalloc", c_int,
+     [POINTER(FleetMoeLayer), c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+      POINTER(FleetMoeDims), c_void_p]),
     ("fleet_attn_workspace_bytes", c_size_t, [POINTER(FleetMoeDims)]),
     ("fleet_attn_decode", c_int,
      [POINTER(FleetAttnLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,

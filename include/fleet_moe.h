@@ -39,6 +39,8 @@ extern "C" {
 #define FLEET_MOE_ERR_ARG 10002       /* null or misaligned pointer, bad count */
 #define FLEET_MOE_ERR_WORKSPACE 10003 /* workspace smaller than required      */
 #define FLEET_MOE_ERR_DEVICE 10004    /* device is not gfx950 / too few CUs   */
+#define FLEET_MOE_ERR_CAPACITY 10005  /* more tokens than the static scratch holds */
+#define FLEET_MOE_ERR_CAPTURE 10006   /* first call on a device made under graph capture */
 
 /* Model scalars, the MoE subset of ModelDims (src/runtime/fleet_types.h:33-39)
  * and of the packed manifest's scalars (src/host/pack_weights.py:153-184). */
@@ -153,6 +155,30 @@ int fleet_moe_grouped(const fleet_moe_layer* layer, int32_t n_tokens, const int3
                       const float* weights, const uint16_t* x_norm, uint16_t* out,
                       void* workspace, size_t workspace_bytes, const fleet_moe_dims* dims,
                       hipStream_t stream);
+
+/* fleet_moe_grouped without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Same kernels, arguments and results as fleet_moe_grouped, but the workspace
+ * is a static device array inside this library (FLEET_MOE_NOALLOC_SCRATCH_BYTES
+ * per device, held until the process ends), laid out for at most
+ * FLEET_MOE_NOALLOC_MAX_TOKENS tokens; n_tokens above that returns
+ * FLEET_MOE_ERR_CAPACITY. Nothing is allocated by any call. The first call on
+ * a device looks up that device's copy of the array and zero-fills it (a fill
+ * kernel on `stream`, then a stream synchronize): it must not be made under
+ * graph capture (FLEET_MOE_ERR_CAPTURE); later calls may be captured.
+ * status: device uint32 that receives the step's FLEET_MOE_ABORT_* bits (0 =
+ * healthy); the array's status word is cleared at the same time, so every
+ * call reports its own. Every call on a device shares that device's array:
+ * calls that overlap in time on one device (two streams, two host threads
+ * without ordering) race and give unspecified results; order them on one
+ * stream. */
+#define FLEET_MOE_NOALLOC_MAX_TOKENS 64
+#define FLEET_MOE_NOALLOC_SCRATCH_BYTES 7574528
+int fleet_moe_grouped_noalloc(const fleet_moe_layer* layer, int32_t n_tokens,
+                              const int32_t* ids, const float* weights, const uint16_t* x_norm,
+                              uint16_t* out, uint32_t* status, const fleet_moe_dims* dims,
+                              hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * The rest of a decoder layer and of the decode step (absorbed MLA attention,

@@ -105,6 +105,25 @@ def test_bad_pointers_rejected_without_device(lib):
     assert lib.fleet_moe_workspace_status(None, None, None) == _lib.ERR_ARG
 
 
+def test_noalloc_grouped_rejects_bad_arguments_without_device(lib):
+    d = c_dims(DSV2_LITE)
+    layer = _lib.FleetMoeLayer(None, 256, 256, DSV2_LITE.expert_stride, 256)
+    n = _lib.NOALLOC_MAX_TOKENS
+    # the stated capacity and the scratch size match the workspace layout
+    assert lib.fleet_moe_grouped_workspace_bytes(ctypes.byref(d), n) == _lib.NOALLOC_SCRATCH_BYTES
+    call = lambda T, status=256: lib.fleet_moe_grouped_noalloc(  # noqa: E731
+        ctypes.byref(layer), T, 256, 256, 256, 256, status, ctypes.byref(d), None)
+    assert call(n + 1) == _lib.ERR_CAPACITY          # beyond the static scratch
+    assert call(4, status=None) == _lib.ERR_ARG      # the status output is required
+    assert call(4, status=258) == _lib.ERR_ARG       # misaligned status
+    assert call(0) == _lib.ERR_ARG
+    bad = c_dims(MoeDims(top_k=8))
+    assert lib.fleet_moe_grouped_noalloc(ctypes.byref(layer), 4, 256, 256, 256, 256, 256,
+                                         ctypes.byref(bad), None) == _lib.ERR_DIMS
+    for code in (_lib.ERR_CAPACITY, _lib.ERR_CAPTURE):
+        assert b"no-allocation" in lib.fleet_moe_error_string(code)
+
+
 def test_attention_entry_points_reject_bad_arguments_without_device(lib):
     d = c_dims(DSV2_LITE)
     n = lib.fleet_attn_workspace_bytes(ctypes.byref(d))
