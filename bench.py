@@ -47,6 +47,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true")
+    ap.add_argument("--no-cold", action="store_true",
+                    help="skip the cold-cache runs (config 1 and the grouped step cycling "
+                         "over 4 distinct MoE layers, 4.7 GB of weights)")
     ap.add_argument("--no-column", action="store_true",
                     help="skip config 3 (27-layer FFN column, 29.8 GB of weights)")
     ap.add_argument("--no-decode", action="store_true",
@@ -92,6 +95,8 @@ def cpu_baseline(blob, lay, x_tok: np.ndarray, budget_s: float, gpu_ids: np.ndar
         pass
     return {
         "value": float(np.median(times)), "unit": "us/layer", "cores": cores, "kind": "port",
+        "tokens": len(times), "p10": round(float(np.percentile(times, 10)), 1),
+        "p90": round(float(np.percentile(times, 90)), 1),
         "sample": f"{len(times)} of config 1's seeded tokens, one MoE layer each "
                   f"(oracle/moe_oracle.moe_layer_fp32: reference_decode.py's fp32 NumPy "
                   f"arithmetic, NumPy {np.__version__}, BLAS threads = "
@@ -223,9 +228,13 @@ def main() -> int:
         # the grouped step takes up to 64 tokens whatever --steps is
         gx = x_host if x_host.shape[0] >= 64 else bf16_tokens(synth, 64)
         result["grouped"] = bench_grouped(torch, dev, stream, layer, dims, gx)
+    del layer
+    torch.cuda.empty_cache()
+    if not args.no_cold:
+        gx = x_host if x_host.shape[0] >= 64 else bf16_tokens(synth, 64)
+        result["cold"] = bench_cold(torch, dev, stream, dims, x_host[:K], gx, lib,
+                                    bytes_layer, args.no_grouped)
     if not args.no_column:
-        del layer
-        torch.cuda.empty_cache()
         result["ffn_column"] = bench_column(torch, dev, stream, dims)
     if not args.no_decode:
         result["full_decode"] = bench_decode(torch, dev, stream, dims)
@@ -247,6 +256,60 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(blob, lay, x_host[:K], args.cpu_seconds, gpu_ids)
     print(json.dumps(result), flush=True)
     return 0 if status == 0 else 1
+
+
+def bench_cold(torch, dev, stream, dims, x_host, gx_host, lib, bytes_layer, no_grouped,
+               n_layers: int = 4, warm: int = 8):
+    """Config 1 and config 2 with no weight reuse through the 256 MB MALL:
+    token t runs MoE layer 1 + t % 4 of a 4-layer stack drawn on the device,
+    so 3 x 138 MB of other layers' weights stream between two uses of a layer
+    (the column and the full decode see the same). The grouped step alternates
+    over the same 4 layers (its T = 4 step reads 260 MB, about the MALL's
+    size, so a single layer would stay partly cached)."""
+    from fleet_moe import _lib, layout as lay_mod, ops, synth_gpu
+    lay = lay_mod.column_layout(dims, n_layers=n_layers + 1)
+    blob = torch.empty(lay.nbytes, dtype=torch.uint8, device=dev)
+    synth_gpu.fill_column(blob, lay, seed=5)
+    layers = [ops.DeviceLayer(blob, lay, i, dims) for i in range(1, n_layers + 1)]
+    cls = [L.c_layer() for L in layers]
+    dec = ops.LayerDecoder(dims, device=dev)
+    xd = torch.from_numpy(x_host).to(dev)
+    y = torch.empty_like(xd[0])
+    cd = ops.c_dims(dims)
+    sh = int(stream.cuda_stream)
+    fn = lib.fleet_moe_layer_decode
+    row = xd.shape[1] * 4
+
+    def launch(t):
+        rc = fn(ctypes.byref(cls[t % n_layers]), xd.data_ptr() + (t % xd.shape[0]) * row,
+                y.data_ptr(), None, None, None, dec.workspace.data_ptr(), dec.workspace.numel(),
+                ctypes.byref(cd), sh)
+        if rc:
+            _lib.check(rc, "fleet_moe_layer_decode")
+
+    for t in range(warm):
+        launch(t)
+    K = xd.shape[0]
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for t in range(K):
+        launch(t)
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / K
+    out = {"workload": f"config 1 cycling over {n_layers} distinct MoE layers (token t on layer "
+                       f"1 + t % {n_layers}), {K} tokens",
+           "us_per_layer": round(us, 3),
+           "hbm_gbs": round(bytes_layer / (us * 1e-6) / 1e9, 1),
+           "frac": round(bytes_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "status": dec.status()}
+    if not no_grouped:
+        out["grouped"] = bench_grouped(torch, dev, stream, layers, dims, gx_host)
+    del layers, dec, blob, xd
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_column(torch, dev, stream, dims, n_tok: int = 32, warm: int = 4):
@@ -413,11 +476,13 @@ def bf16_tokens(synth, n):
             & 0xFFFF0000).astype(np.uint32).view(np.float32)
 
 
-def bench_grouped(torch, dev, stream, layer, dims, x_host):
+def bench_grouped(torch, dev, stream, layers, dims, x_host):
     """Config 2: T in {4, 16, 64}, Zipf(1.1)-biased routing; times the grouped
-    product alone (routing precomputed), per step."""
+    product alone (routing precomputed), per step. `layers`: one DeviceLayer,
+    or a list the steps cycle over (one step per layer in turn)."""
     from fleet_moe import ops, synth
     out = {}
+    layers = layers if isinstance(layers, list) else [layers]
     bias = torch.from_numpy(synth.zipf_logit_bias(0)).to(dev)
     runner = ops.GroupedRunner(64, dims, device=dev)
     for T in (4, 16, 64):
@@ -429,22 +494,24 @@ def bench_grouped(torch, dev, stream, layer, dims, x_host):
         xf = x.double()
         xn = x * torch.rsqrt((xf * xf).mean(-1, keepdim=True).float() + dims.rms_eps)
         xn = ops.bf16_bits_to_f32(ops.f32_to_bf16_bits(xn)).contiguous()
-        _, ids, ws = ops.route(layer, xn, bias)
+        routes = [ops.route(L, xn, bias)[1:] for L in layers]
         xb = ops.f32_to_bf16_bits(xn).contiguous()
         o = torch.empty((T, dims.hidden), dtype=torch.int16, device=dev)
-        for _ in range(5):
-            runner.run_into(layer, xb, ids, ws, o)
+        nl = len(layers)
+        for i in range(5 * nl):
+            runner.run_into(layers[i % nl], xb, *routes[i % nl], o)
         torch.cuda.synchronize()
-        n = 50
+        n = 48 if nl > 1 else 50
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        for _ in range(n):
-            runner.run_into(layer, xb, ids, ws, o)
+        for i in range(n):
+            runner.run_into(layers[i % nl], xb, *routes[i % nl], o)
         b.record(stream)
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / n
-        distinct = int(torch.unique(ids).numel())
+        dist = [int(torch.unique(r[0]).numel()) for r in routes]
+        distinct = float(np.mean(dist)) if nl > 1 else dist[0]
         nbytes = distinct * 3 * dims.hidden * dims.moe_inter * 2 + 3 * dims.hidden * dims.shared_inter * 2
         flops = 2.0 * T * (6 * 3 * dims.hidden * dims.moe_inter + 3 * dims.hidden * dims.shared_inter)
         out[f"T{T}"] = {"us_per_step": round(us, 2), "distinct_experts": distinct,
