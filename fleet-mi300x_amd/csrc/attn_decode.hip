@@ -91,7 +91,7 @@ static_assert(kBatch <= kLanes, "one lane per row for the exponentials");
 
 struct Workspace {
     uint32_t epoch;                            // calls completed on this workspace
-    uint32_t exits;                            // workgroup exits over all calls
+    uint32_t pad0;
     uint32_t abort;                            // offset 8: sticky status
     uint32_t pad1[61];
     float qkv[kQkvRows];                       // plain copies of the published values
@@ -863,6 +863,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         reinterpret_cast<uint2*>(L.u.s5.outv)[64 * wave + lane] =
             make_uint2((v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16));
         __syncthreads();
+        // Every workgroup published its head outputs with this call's tag, so
+        // every one has read the call count: workgroup 0 can advance it now,
+        // for the next call (which starts after this launch has ended).
+        if (wg == 0 && tid == 0) st_agent(&ws->epoch, epoch);
         const u32x4* hv = reinterpret_cast<const u32x4*>(L.u.s5.outv + 256 * wave + 32 * (lane & 7));
         double a = 0.0;
 #pragma unroll
@@ -878,11 +882,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         }
     }
     ATTN_TRACE(15);
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&ws->epoch, epoch);
-    }
 }
 
 // ---------------------------------------------------------------- embed / lm_head / argmax

@@ -84,7 +84,7 @@ constexpr uint32_t kAbortRouteMismatch = 0x100u;
 // offsets fleet_moe_workspace_status relies on.
 struct Workspace {
     uint32_t epoch;        // calls completed on this workspace
-    uint32_t exits;        // workgroup exits over all calls
+    uint32_t pad_exits;
     uint32_t abort;        // sticky FLEET_MOE_ABORT_* bits
     uint32_t pad0[61];
     uint64_t logit[kRouted];   // (epoch << 32) | fp32 exact logit bits
@@ -785,11 +785,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
         if (P.ids_out) P.ids_out[tid] = L.ids[k];
         if (P.w_out) P.w_out[tid] = L.w[k];
     }
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&ws->epoch, epoch);
-    }
+    // Every workgroup published h words with this call's tag (each unit's
+    // pairs are spread over all of them), and this workgroup has seen all of
+    // them, so every workgroup has read the call count: workgroup 0 advances
+    // it for the next call (which starts after this launch has ended).
+    if (wg == 0 && tid == 0) st_agent(&ws->epoch, epoch);
     FLEET_TRACE(7);
 }
 

@@ -40,7 +40,7 @@ static_assert(kDenseInter % 4 == 0, "h polled in 16-byte units");
 
 struct Workspace {
     uint32_t epoch;
-    uint32_t exits;
+    uint32_t pad_exits;
     uint32_t abort;
     uint32_t pad0[61];
     uint32_t h[kDenseInter];   // (epoch & 0xffff) << 16 | bf16 h
@@ -211,6 +211,9 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
         __hip_atomic_fetch_or(&ws->abort, FLEET_MOE_ABORT_UNIT_WAIT, __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+    // every workgroup's h words carried this call's tag, so every workgroup
+    // has read the call count: workgroup 0 advances it for the next call
+    if (wg == 0 && tid == 0) st_agent(&ws->epoch, epoch);
     // bf16(down . h) exactly rounded: certified fp32 evaluation (v_dot2
     // chain 8, a 22-value tree 5, wave sum 6), exact fp64 sum as fallback
     u32x4 hv[kDnIters];
@@ -242,12 +245,6 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     if (lane == 0) {
         P.x_out[n] = bf16r(P.x[n] + out);
         if (P.mlp_out) P.mlp_out[n] = (uint16_t)bf16_bits(out);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&ws->exits, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * (uint32_t)kWG) st_agent(&ws->epoch, epoch);
     }
 }
 
