@@ -84,6 +84,11 @@ constexpr int kQcCols = kLora / kChunks;                 // 32 columns of q_c / 
 constexpr int kUkRows = kNope / kWaves;                  // 16 W_UK rows per wave
 constexpr int kUvRows = kV / kChunks;                    // 8 W_UV rows per workgroup
 constexpr int kOpRows = kHidden / kWG;                   // 8 o_proj rows per workgroup
+// The head outputs are read by every workgroup (S5): they are published in
+// kOutCopies copies and workgroup w polls copy w % kOutCopies, so each line
+// sees 32 pollers instead of 256 (same-address device-scope requests queue at
+// the line's memory channel).
+constexpr int kOutCopies = 8;
 constexpr int kBatch = 9;                                // cache rows a wave holds at once (72-row chunks: one batch)
 static_assert(kHeads * kChunks == kWG && kQcCols * kChunks == kLora, "work split");
 static_assert(kUvRows == kWaves && kOpRows == kWaves, "one row per wave in the epilogues");
@@ -108,7 +113,7 @@ struct Workspace {
     uint32_t ml_t[kHeads][kChunks][8];         // fp64 chunk max, then fp64 chunk sum of exp
     uint32_t o_t[kHeads][kChunks][kLora][4];   // fp64 chunk sum of exp * c
     uint32_t oc_t[kHeads][kLora][2];           // fp32 o_c
-    uint32_t out_t[kHeads * kV];               // bf16 head outputs
+    uint32_t out_t[kOutCopies][kHeads * kV];   // bf16 head outputs, kOutCopies copies
     float cand_v[kWG];                         // lm_head: best logit per workgroup
     int32_t cand_i[kWG];
 };
@@ -342,13 +347,13 @@ __device__ __forceinline__ double dot8_xd(const u32x4& w, const double* x, doubl
 // -ffp-contract=fast, and its __fmul_rn / __fadd_rn carry that flag into the
 // inlined code): a fused multiply-add rounds twice instead of three times and
 // moves about one result in 2^16 to the neighbouring bf16 value.
-__device__ __forceinline__ float rope_one(const float* v, const float* cs, const float* sn, int i) {
+__device__ __forceinline__ float rope_one(const float* v, float cs_i, float sn_i, int i) {
 #pragma clang fp contract(off)
     const int half = kRope / 2;
     const float y = i < half ? v[2 * i] : v[2 * (i - half) + 1];
     const float r = i < half ? -v[2 * i + 1] : v[2 * (i - half)];
-    const float a = y * cs[i];
-    const float b = r * sn[i];
+    const float a = y * cs_i;
+    const float b = r * sn_i;
     return bf16r(a + b);
 }
 
@@ -500,12 +505,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     const bool last = k == n_used - 1;                  // the chunk holding `pos`
 
     // ---- the inputs of the first stage
-    const uint32_t epoch = ld_agent(&ws->epoch) + 1u;
+    // the call count, written by the previous launch: a plain load (after the
+    // launch boundary it is current; device-scope loads of one word by every
+    // wave would queue at its memory channel)
+    const uint32_t epoch = ws->epoch + 1u;
     const uint32_t tag = (epoch & 0xffffu) << 16;
     const float4 xv = reinterpret_cast<const float4*>(P.x)[tid];
     const uint2 gb = P.norm_in ? reinterpret_cast<const uint2*>(P.norm_in)[tid]
                                : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
     const float x_own = tid < kOpRows ? P.x[kOpRows * wg + tid] : 0.f;
+    // S3's per-position inputs, needed after several hand-offs: this
+    // position's RoPE angle (thread i < 64: element i) and the kv_a_layernorm
+    // weight (thread i: element i)
+    const float cs_t = tid < kRope ? P.cos[(int64_t)pos * kRope + tid] : 0.f;
+    const float sn_t = tid < kRope ? P.sin[(int64_t)pos * kRope + tid] : 0.f;
+    const float kvn_t = P.kv_a_norm ? __uint_as_float((uint32_t)P.kv_a_norm[tid] << 16) : 1.0f;
     // q rows of head h: 12 per workgroup (i = wave, and wave + 8 for waves
     // 0..3); kv_a rows: 3072 + wg + 256 i for waves 4..6 (i = wave - 4, the
     // last only for wg < 64)
@@ -625,8 +639,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     ATTN_TRACE(5);
 
     // ---- S3: the chunk's scores and fp64 softmax partial
-    const float* cs = P.cos + (int64_t)pos * kRope;
-    const float* sn = P.sin + (int64_t)pos * kRope;
     if (has_rows) {
         u32x4 v;
         if (wave < 4) {
@@ -659,7 +671,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         ATTN_TRACE(6);
         __syncthreads();
         if (tid < kRope) {
-            const float qp = rope_one(L.u.s3.qpe_raw, cs, sn, tid);
+            const float qp = rope_one(L.u.s3.qpe_raw, cs_t, sn_t, tid);
             L.u.s3.qpe[tid] = qp;
             if (k == 0) ws->qpe[h][tid] = qp;
         }
@@ -674,12 +686,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             for (int w = 0; w < kWaves; ++w) ssq += L.red[w];
             const float var = (float)(ssq / (double)kLora);
             const float inv = __fdiv_rn(1.0f, sqrt_rn(var + P.eps));
-            const float g = P.kv_a_norm ? __uint_as_float((uint32_t)P.kv_a_norm[tid] << 16) : 1.0f;
+            const float g = kvn_t;
             const uint16_t cb = (uint16_t)bf16_bits(bf16r(bf16r(c * inv) * g));
             L.u.s3.row[tid] = cb;
             uint16_t kb = 0;
             if (tid < kRope) {
-                kb = (uint16_t)bf16_bits(rope_one(L.u.s3.kva + kLora, cs, sn, tid));
+                kb = (uint16_t)bf16_bits(rope_one(L.u.s3.kva + kLora, cs_t, sn_t, tid));
                 L.u.s3.row[kLora + tid] = kb;
             }
             if (h == 0) {
@@ -689,6 +701,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             }
         }
         __syncthreads();
+        ATTN_TRACE(7);
 
         double qd[8];
 #pragma unroll
@@ -849,7 +862,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) s += L.u.s4.uvr[w][tid];
             const float ob = bf16r((float)s);
-            st_agent(&ws->out_t[h * kV + kUvRows * k + tid], tag | bf16_bits(ob));
+            const uint32_t word = tag | bf16_bits(ob);
+#pragma unroll
+            for (int c = 0; c < kOutCopies; ++c)
+                st_agent(&ws->out_t[c][h * kV + kUvRows * k + tid], word);
         }
         __syncthreads();
     }
@@ -858,7 +874,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     // ---- S5: o_proj rows 8 wg .. 8 wg + 7 and the residual add
     {
         u32x4 v;
-        poll16(ws->out_t, 4 * (256 * wave + 4 * lane), true, tag, v, ws);
+        poll16(ws->out_t[wg % kOutCopies], 4 * (256 * wave + 4 * lane), true, tag, v, ws);
         ATTN_TRACE(14);
         reinterpret_cast<uint2*>(L.u.s5.outv)[64 * wave + lane] =
             make_uint2((v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16));

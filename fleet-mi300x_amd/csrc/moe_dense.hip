@@ -83,7 +83,10 @@ __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     const int wg = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & (kLanes - 1);
     Workspace* ws = P.ws;
-    const uint32_t epoch = ld_agent(&ws->epoch) + 1u;
+    // the call count, written by the previous launch: a plain load (current
+    // after the launch boundary; a device-scope load of one word by every
+    // wave would queue at its memory channel)
+    const uint32_t epoch = ws->epoch + 1u;
     const uint32_t tag = (epoch & 0xffffu) << 16;
     const float4 xv = reinterpret_cast<const float4*>(P.x)[tid];
     const uint2 gb = P.norm ? reinterpret_cast<const uint2*>(P.norm)[tid]
