@@ -7,9 +7,16 @@ The GPU runs the whole thing as the benchmark does (graph replays, token and
 position on the device). The oracle decodes from the GPU's prefilled KV cache
 (a NumPy prefill of 1024 positions x 27 layers would take most of an hour):
 it recomputes the last prompt step itself, which re-derives cache row 1023 of
-every layer (compared with the GPU's row within bf16 tolerance) and the first
-pick, then runs the 32 greedy steps on its own state. The routed experts a
-step needs are read back from the device as the oracle asks for them."""
+every layer and the first pick, then runs the 32 greedy steps on its own
+state. The routed experts a step needs are read back from the device as the
+oracle asks for them.
+
+The prefill itself is checked teacher-forced at sampled positions (0, 255,
+511, 1023): those steps run eagerly, layer by layer, recording every layer's
+input and its residual after attention, and for all 27 layers the oracle,
+given the GPU's input and the GPU's cache rows before the position, must
+reproduce bit for bit the appended cache row and the attention half (at every
+sampled position) and the FFN half (dense or MoE; at positions 0 and 1023)."""
 from __future__ import annotations
 
 import numpy as np
@@ -84,6 +91,55 @@ def oracle_model(dec: ops.Decoder) -> orc.DecodeModel:
                            lm_head=orc.bf16_to_f32(f("lm_head")), attn=attn, ffn=ffn)
 
 
+SAMPLED = (0, 255, 511, PROMPT - 1)
+FFN_SAMPLED = (0, PROMPT - 1)
+
+
+def eager_step_recording(dec: ops.Decoder):
+    """One decode step launched layer by layer (the kernels a graph replay
+    runs, in the same order), recording each layer's input and its residual
+    after the attention half. Returns fp32 [layers + 1][H] inputs (the last
+    one: the final residual) and [layers][H] mid residuals, on the host."""
+    x = dec.x
+    ins, mids = [], []
+    dec.attn.embed_into(dec._addr("embed"), dec.token, x)
+    for i in range(dec.n_layers):
+        ins.append(x.clone())
+        dec.attn.attn_into(dec.attn_layers[i], x, x, dec.cache[i], 0, dec.pos, dec.cos, dec.sin)
+        mids.append(x.clone())
+        dec.ffn.layer_into(i, x, x)
+    ins.append(x.clone())
+    dec.attn.lm_head_into(x, dec._addr("final_norm"), dec._addr("lm_head"), None, dec.token_out,
+                          dec.token, dec.pos)
+    return torch.stack(ins).cpu().numpy(), torch.stack(mids).cpu().numpy()
+
+
+def check_prefill_teacher_forced(m: orc.DecodeModel, g_cache, records, cos, sin):
+    """Bit-exact teacher-forced checks of the recorded prefill steps."""
+    for p, (ins, mids) in records.items():
+        for i in range(LAYERS):
+            cache = np.zeros((p + 1, 576), np.float32)
+            cache[:p] = orc.bf16_to_f32(g_cache[i, :p])
+            a = orc.attention(m.attn[i], ins[i], cache, p, cos, sin)
+            g_row = orc.bf16_to_f32(g_cache[i, p])
+            np.testing.assert_array_equal(g_row.view(np.uint32), a["row"].view(np.uint32),
+                                          err_msg=f"cache row {p} of layer {i}")
+            x1 = orc.bf16_round(ins[i] + a["out"])
+            np.testing.assert_array_equal(mids[i].view(np.uint32), x1.view(np.uint32),
+                                          err_msg=f"attention half, layer {i} pos {p}")
+            if p in FFN_SAMPLED:
+                f = m.ffn[i]
+                if isinstance(f, orc.DenseFfn):
+                    want = orc.dense_layer(f.gate, f.up, f.down, mids[i],
+                                           orc.bf16_to_f32(f.norm))["x_out"]
+                else:
+                    want = orc.moe_layer(f, mids[i])["x_out"]
+                np.testing.assert_array_equal(ins[i + 1].view(np.uint32), want.view(np.uint32),
+                                              err_msg=f"FFN half, layer {i} pos {p}")
+        say(f"prefill position {p}: cache rows, attention"
+            f"{' and FFN' if p in FFN_SAMPLED else ''} of all {LAYERS} layers bit-exact")
+
+
 @pytest.mark.timeout(900)
 def test_full_decode_32_greedy_tokens_match_oracle():
     lay = lay_mod.model_layout(DSV2_LITE, n_layers=LAYERS)
@@ -94,8 +150,16 @@ def test_full_decode_32_greedy_tokens_match_oracle():
     dec = ops.Decoder(blob, lay, DSV2_LITE, max_pos=max_pos)
     prompt = np.random.default_rng(0).integers(0, V, PROMPT).astype(np.int32)
     dec.capture()
-    say("gpu prefill")
-    dec.prefill(torch.from_numpy(prompt).cuda())
+    say("gpu prefill (graph replays; eager and recorded at the sampled positions)")
+    prompt_d = torch.from_numpy(prompt).cuda()
+    dec.reset(0)
+    records = {}
+    for p in range(PROMPT):
+        dec.token.copy_(prompt_d[p:p + 1])
+        if p in SAMPLED:
+            records[p] = eager_step_recording(dec)
+        else:
+            dec.step()
     tok0 = int(dec.token_out.item())
     g_cache = dec.cache[:, :PROMPT].cpu().numpy().view(np.uint16)
     say("gpu generate")
@@ -107,6 +171,7 @@ def test_full_decode_32_greedy_tokens_match_oracle():
     say("oracle weights")
     m = oracle_model(dec)
     cos, sin = rope.yarn_tables(max_pos)
+    check_prefill_teacher_forced(m, g_cache, records, cos, sin)
     caches = []
     for i in range(LAYERS):
         c = np.zeros((max_pos, 576), np.float32)
