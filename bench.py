@@ -54,11 +54,69 @@ def parse_args():
                     help="skip config 3 (27-layer FFN column, 29.8 GB of weights)")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip config 4 (27-layer full decode, 31.4 GB of weights)")
+    ap.add_argument("--no-attention", action="store_true",
+                    help="skip the attention-layer and lm_head legs (config 4's kernels alone)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the known-size kernels that scale rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE: fleet_moe_stream_read over 256 MiB and a 64 MiB fill, "
                          "3 launches each")
     return ap.parse_args()
+
+
+COUNTERS = ROOT / "profiles" / "kernel_counters.json"
+
+
+def load_counters() -> dict:
+    """Per-leg HBM bytes and MFMA busy cycles per launch or step, from the
+    committed rocprofv3 counter passes (FETCH_SIZE / WRITE_SIZE calibrated
+    against known-size kernels, SQ_VALU_MFMA_BUSY_CYCLES)."""
+    try:
+        return json.loads(COUNTERS.read_text())["kernels"]
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
+def counter_view(result: dict, profiled: dict) -> dict:
+    """The profiled bytes (and MFMA busy cycles) of each leg over this run's
+    own time for it: counter-derived GB/s and MFMA busy fraction."""
+    def get(*path):
+        v = result
+        for p in path:
+            if not isinstance(v, dict) or p not in v:
+                return None
+            v = v[p]
+        return v
+
+    col = get("ffn_column", "us_per_token")
+    dense = get("ffn_column", "dense_layer", "us")
+    times = {
+        "moe_layer": get("roofline", "kernel_us_mean"),
+        "moe_layer_cold": get("cold", "us_per_layer"),
+        "attention": get("attention", "us_cold"),
+        "lm_head": get("attention", "lm_head", "us"),
+        "dense": dense,
+        "moe_layer_in_column": (col - dense) / 26 if col and dense else None,
+    }
+    for t in ("T4", "T16", "T64"):
+        times[f"grouped_{t}"] = get("grouped", t, "us_per_step")
+        times[f"grouped_{t}_cold"] = get("cold", "grouped", t, "us_per_step")
+    out = {"source": "profiles/kernel_counters.json"}
+    for name, us in times.items():
+        p = profiled.get(name)
+        if not p or not us:
+            continue
+        e = {"hbm_bytes": p["hbm_bytes"], "traffic_over_algorithmic": p["traffic_over_algorithmic"],
+             "us": round(us, 3), "counter_gbs": round(p["hbm_bytes"] / (us * 1e-6) / 1e9, 1),
+             "counter_frac": round(p["hbm_bytes"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if "mfma_busy_cycles" in p:
+            e["mfma_busy_frac"] = round(p["mfma_busy_cycles"] / (1024 * us * 1e-6 * 2.4e9), 5)
+        out[name] = e
+    return out
+
+
+def progress(msg: str) -> None:
+    """One line per finished leg on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def cpu_baseline(blob, lay, x_tok: np.ndarray, budget_s: float, gpu_ids: np.ndarray):
@@ -182,15 +240,11 @@ def main() -> int:
     k_mean = total_ms * 1e3 / K
     achieved = bytes_layer / (k_mean * 1e-6) / 1e9
 
-    traffic = None
-    tf = ROOT / "profiles" / "moe_decode_traffic.json"
-    if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+    profiled = load_counters()
+    traffic = profiled.get("moe_layer", {}).get("hbm_bytes")
 
     gpu_ids = ids.cpu().numpy()
+    progress(f"config 1: {us_layer:.3f} us/layer")
     result = {
         "metric": METRIC,
         "value": round(us_layer, 3),
@@ -228,16 +282,23 @@ def main() -> int:
         # the grouped step takes up to 64 tokens whatever --steps is
         gx = x_host if x_host.shape[0] >= 64 else bf16_tokens(synth, 64)
         result["grouped"] = bench_grouped(torch, dev, stream, layer, dims, gx)
+        progress("grouped steps done")
     del layer
     torch.cuda.empty_cache()
     if not args.no_cold:
         gx = x_host if x_host.shape[0] >= 64 else bf16_tokens(synth, 64)
         result["cold"] = bench_cold(torch, dev, stream, dims, x_host[:K], gx, lib,
                                     bytes_layer, args.no_grouped)
+        progress("cold legs done")
+    if not args.no_attention:
+        result["attention"] = bench_attention(torch, dev, stream, dims)
+        progress("attention and lm_head legs done")
     if not args.no_column:
         result["ffn_column"] = bench_column(torch, dev, stream, dims)
+        progress("FFN column done")
     if not args.no_decode:
         result["full_decode"] = bench_decode(torch, dev, stream, dims)
+        progress("full decode done")
     result["stream_read"] = stream_ceiling(torch, dev, stream, lib)
     if args.calibrate:
         n = 256 << 20
@@ -252,6 +313,7 @@ def main() -> int:
         torch.cuda.synchronize()
         result["calibration"] = {"stream_read_bytes": n, "fill_bytes": 64 << 20, "launches": 3}
 
+    result["counters"] = counter_view(result, profiled)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(blob, lay, x_host[:K], args.cpu_seconds, gpu_ids)
     print(json.dumps(result), flush=True)
@@ -442,6 +504,104 @@ def bench_decode(torch, dev, stream, dims, prompt_len: int = 1024, n_gen: int = 
     del dec, blob
     torch.cuda.empty_cache()
     return out
+
+
+def bench_attention(torch, dev, stream, dims, pos: int = 1024, n_layers: int = 12,
+                    rounds: int = 8, warm_launches: int = 50, head_launches: int = 20):
+    """Config 4's per-layer attention kernel and its lm_head kernel alone.
+
+    Attention: `n_layers` independent layers (qkv, kv_b, o_proj drawn
+    N(0, 0.02^2), unit norms; 12 x 28.7 MB exceeds the 256 MB MALL), each with
+    a KV cache whose rows 0..pos-1 are N(0,1) bf16, one call per layer in turn
+    at position `pos` (the position the decode benchmark's tokens start at):
+    the cold figure. The warm figure repeats layer 0 back to back.
+    lm_head: final RMSNorm + the 102400 x 2048 GEMV + argmax (420 MB, always
+    cold), back to back."""
+    from fleet_moe import layout as lay_mod, ops
+    from fleet_moe.rope import yarn_tables
+    H = dims.hidden
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+
+    def normal(n, std=0.02):
+        return (torch.randn(n, generator=g, device=dev) * std).to(torch.bfloat16).view(torch.int16)
+
+    one = torch.tensor(1.0, dtype=torch.bfloat16).view(torch.int16).item()
+    kv_rows = lay_mod.ATTN_HEADS * (lay_mod.QK_NOPE + lay_mod.V_HEAD)
+    w_bytes = (lay_mod.QKV_ROWS * H + kv_rows * lay_mod.KV_LORA
+               + H * lay_mod.ATTN_HEADS * lay_mod.V_HEAD) * 2
+    layers, keep = [], []
+    max_pos = pos + 64
+    for _ in range(n_layers):
+        t = {"norm_in": torch.full((H,), one, dtype=torch.int16, device=dev),
+             "qkv": normal(lay_mod.QKV_ROWS * H),
+             "kv_a_norm": torch.full((lay_mod.KV_LORA,), one, dtype=torch.int16, device=dev),
+             "kv_b": normal(kv_rows * lay_mod.KV_LORA),
+             "o_proj": normal(H * lay_mod.ATTN_HEADS * lay_mod.V_HEAD),
+             "cache": torch.zeros((max_pos, 576), dtype=torch.int16, device=dev)}
+        t["cache"][:pos] = normal(pos * 576, 1.0).view(pos, 576)
+        keep.append(t)
+        layers.append(ops._lib.FleetAttnLayer(t["norm_in"].data_ptr(), t["qkv"].data_ptr(),
+                                              t["kv_a_norm"].data_ptr(), t["kv_b"].data_ptr(),
+                                              t["o_proj"].data_ptr()))
+    cos, sin = yarn_tables(max_pos)
+    cos, sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    ad = ops.AttnDecoder(dims, device=dev)
+    x = torch.randn(H, generator=g, device=dev).to(torch.bfloat16).float()
+    y = torch.empty_like(x)
+
+    def timed(fn, n):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(n):
+            fn(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / n
+
+    def call(i):
+        k = i % n_layers
+        ad.attn_into(layers[k], x, y, keep[k]["cache"], pos, None, cos, sin, stream)
+
+    for i in range(2 * n_layers):
+        call(i)
+    torch.cuda.synchronize()
+    us_cold = timed(call, rounds * n_layers)
+    us_warm = timed(lambda i: call(0), warm_launches)
+    # algorithmic bytes: the weights, the norms, the pos cached rows read and
+    # the new row written
+    a_bytes = w_bytes + (H + lay_mod.KV_LORA) * 2 + (pos + 1) * 576 * 2
+    status = ad.status()
+    del keep, layers
+    # lm_head: 102400 x 2048 bf16
+    head = normal(lay_mod.VOCAB * H)
+    fnorm = torch.full((H,), one, dtype=torch.int16, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        ad.lm_head_into(x, fnorm.data_ptr(), head.data_ptr(), None, tok, None, None, stream)
+    torch.cuda.synchronize()
+    us_head = timed(lambda i: ad.lm_head_into(x, fnorm.data_ptr(), head.data_ptr(), None, tok,
+                                              None, None, stream), head_launches)
+    h_bytes = lay_mod.VOCAB * H * 2 + H * 2
+    status |= ad.status()
+    del head
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"config 4's attention half alone (absorbed MLA, 16 heads, KV cache of {pos} "
+                    f"rows, one call at position {pos}); cold: {n_layers} layers in turn "
+                    f"({n_layers * w_bytes / 1e6:.0f} MB of weights between reuses), warm: one "
+                    "layer back to back",
+        "us_cold": round(us_cold, 2), "us_warm": round(us_warm, 2), "bytes": a_bytes,
+        "hbm_gbs": round(a_bytes / (us_cold * 1e-6) / 1e9, 1),
+        "frac": round(a_bytes / (us_cold * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernel": "fleet_moe::attn::attn_layer_kernel",
+        "lm_head": {"us": round(us_head, 2), "bytes": h_bytes,
+                    "hbm_gbs": round(h_bytes / (us_head * 1e-6) / 1e9, 1),
+                    "frac": round(h_bytes / (us_head * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "kernels": "fleet_moe::attn::lmhead_kernel + argmax_kernel"},
+        "status": status,
+    }
 
 
 def stream_ceiling(torch, dev, stream, lib):
