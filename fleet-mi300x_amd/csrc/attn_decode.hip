@@ -25,22 +25,24 @@
 //             in workgroup j % 256.
 //   S2 q_c    workgroup (h, k): columns 32k .. 32k+31 of head h's absorbed
 //             query q_c = W_UK^T q_nope (128 rows x 32 columns of W_UK).
-//   S3 mla    workgroup (h, k): positions chunk k of head h (16 chunks of
+//   S3 mla    workgroup (h3, k3): positions chunk k3 of head h3 (16 chunks of
 //             ceil((pos+1)/16)): scores, then the chunk's fp64 softmax partial
 //             (max, sum of exp, sum exp * c); the workgroups holding the
 //             current position derive its cache row (kv_a_layernorm of c,
-//             RoPE of k_pe) from kv_a themselves, and (0, k) writes it.
+//             RoPE of k_pe) from kv_a themselves, and (0, k3) writes it.
 //   S4 merge  workgroup (h, k): columns 32k .. 32k+31 of o_c merged from the
 //             chunk partials and rounded once; then rows 8k .. 8k+7 of
 //             W_UV o_c, bf16.
 //   S5 oproj  workgroup w: rows 8w .. 8w+7 of o_proj, bf16, residual add.
-// Workgroup w has (h, k) = (w % 8 + 8 ((w / 8) % 2), w / 16): workgroups are
-// dealt to the 8 XCDs round-robin (w % 8), so all 16 workgroups of a head
-// share one XCD, and what passes between them (its q rows, q_c, the chunk
-// partials, o_c) is written and polled through that XCD's L2: a
-// device-scope poll on the producer's XCD sees the word sooner than one on
-// another XCD. Every word is published with a device-scope store, so the
-// protocol does not depend on that placement, only its speed does.
+// Workgroup w has (h, k) = (w % 8 + 8 ((w / 8) % 2), w / 16) in S1, S2, S4
+// and S5: workgroups are dealt to the 8 XCDs round-robin (w % 8), so all 16
+// workgroups of a head share one XCD and its q rows, q_c and o_c pass through
+// that XCD. In S3 it has (h3, k3) = ((w / 8) % 16, 2 (w % 8) + w / 128): XCD
+// x takes position chunks 2x and 2x + 1 of every head, so each cached row is
+// fetched from HBM into one XCD's L2 (which serves it to all 16 heads)
+// instead of into all eight. Every word is published with a device-scope
+// store, so the protocol does not depend on the placement, only its speed
+// does.
 // The position can come from the host (an argument) or from device memory
 // (pos_dev), so a whole decode step can be captured once in a HIP graph and
 // replayed: the argmax kernel then advances *pos_dev itself. A device
@@ -499,10 +501,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     const int n_pos = pos + 1;
     const int C = (n_pos + kChunks - 1) / kChunks;      // positions per chunk
     const int n_used = (n_pos + C - 1) / C;             // chunks holding positions
-    const int t0 = k * C;
+    // S3's (head, chunk): XCD x (wg % 8) takes chunks 2x and 2x + 1 of all 16 heads, so
+    // each cached row is fetched into one XCD's L2 only
+    const int h3 = (wg >> 3) & 15;
+    const int k3 = 2 * (wg & 7) + (wg >> 7);
+    const int t0 = k3 * C;
     const int t1 = min(t0 + C, n_pos);
-    const bool has_rows = k < n_used;
-    const bool last = k == n_used - 1;                  // the chunk holding `pos`
+    const bool has_rows = k3 < n_used;
+    const bool last = k3 == n_used - 1;                 // the chunk holding `pos`
 
     // ---- the inputs of the first stage
     // the call count, written by the previous launch: a plain load (after the
@@ -555,9 +561,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
         }
     }
 
-    // The other stages' weight slices and cache rows go in flight now, behind
-    // the first stage's inputs: issued before the RMSNorm, these ~30 loads
-    // per wave would hold up x and the q / kv_a rows.
+    // S2's weight slice and S3's cache rows go in flight now, behind the first
+    // stage's inputs: issued before the RMSNorm, these ~10 loads per wave
+    // would hold up x and the q / kv_a rows.
     // W_UK of head h: row 16 wave + lane / 4, columns 32 k + 8 (lane % 4) .. + 7
     const u32x4 wuk = ld_stream(reinterpret_cast<const u32x4*>(
         P.kv_b + ((int64_t)h * kKvbRowsPerHead + kUkRows * wave + (lane >> 2)) * kLora +
@@ -578,19 +584,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             c8[i] = u32x4{0u, 0u, 0u, 0u};
             kp[i] = 0.f;
         }
-    }
-    // W_UV of head h: row 8 k + lane / 8, columns 64 wave + 8 (lane % 8) .. + 7
-    const u32x4 wuv = ld_stream(reinterpret_cast<const u32x4*>(
-        P.kv_b + ((int64_t)h * kKvbRowsPerHead + kNope + kUvRows * k + (lane >> 3)) * kLora +
-        64 * wave + 8 * (lane & 7)));
-    // o_proj: row 8 wg + lane / 8, columns 256 wave + 32 (lane % 8) .. + 31
-    u32x4 wo[4];
-    {
-        const u32x4* p = reinterpret_cast<const u32x4*>(
-            P.o_proj + (int64_t)(kOpRows * wg + (lane >> 3)) * kHidden + 256 * wave +
-            32 * (lane & 7));
-#pragma unroll
-        for (int m = 0; m < 4; ++m) wo[m] = ld_stream(p + m);
     }
 
     ATTN_TRACE(3);
@@ -639,16 +632,32 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     ATTN_TRACE(5);
 
     // ---- S3: the chunk's scores and fp64 softmax partial
+    // S4's and S5's weight slices go in flight once this stage's polls are
+    // done: issued earlier, they would sit ahead of the polls (a wave's loads
+    // complete in order) and ahead of the cache rows in the memory queues.
+    u32x4 wuv, wo[4];
+    auto load_tail = [&]() {
+        // W_UV of head h: row 8 k + lane / 8, columns 64 wave + 8 (lane % 8) .. + 7
+        wuv = ld_stream(reinterpret_cast<const u32x4*>(
+            P.kv_b + ((int64_t)h * kKvbRowsPerHead + kNope + kUvRows * k + (lane >> 3)) * kLora +
+            64 * wave + 8 * (lane & 7)));
+        // o_proj: row 8 wg + lane / 8, columns 256 wave + 32 (lane % 8) .. + 31
+        const u32x4* p = reinterpret_cast<const u32x4*>(
+            P.o_proj + (int64_t)(kOpRows * wg + (lane >> 3)) * kHidden + 256 * wave +
+            32 * (lane & 7));
+#pragma unroll
+        for (int m = 0; m < 4; ++m) wo[m] = ld_stream(p + m);
+    };
     if (has_rows) {
         u32x4 v;
         if (wave < 4) {
             // q_c of head h: 512 tagged words, 2 per lane
-            poll16(ws->qc_t, 8 * (h * kLora + 128 * wave + 2 * lane), true, tag, v, ws);
+            poll16(ws->qc_t, 8 * (h3 * kLora + 128 * wave + 2 * lane), true, tag, v, ws);
             L.u.s3.qc[128 * wave + 2 * lane] = tagged_f32(v.x, v.y);
             L.u.s3.qc[128 * wave + 2 * lane + 1] = tagged_f32(v.z, v.w);
         } else if (wave == 4) {
             // q_pe of head h before RoPE: 64 words, 4 per lane
-            poll16(ws->qkv_t, 4 * (h * (kNope + kRope) + kNope) + 16 * lane, lane < 16,
+            poll16(ws->qkv_t, 4 * (h3 * (kNope + kRope) + kNope) + 16 * lane, lane < 16,
                    tag, v, ws);
             if (lane < 16) {
                 L.u.s3.qpe_raw[4 * lane] = __uint_as_float(v.x << 16);
@@ -669,11 +678,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             }
         }
         ATTN_TRACE(6);
+        load_tail();
         __syncthreads();
         if (tid < kRope) {
             const float qp = rope_one(L.u.s3.qpe_raw, cs_t, sn_t, tid);
             L.u.s3.qpe[tid] = qp;
-            if (k == 0) ws->qpe[h][tid] = qp;
+            if (k3 == 0) ws->qpe[h3][tid] = qp;
         }
         if (last) {
             // c = kv_a_layernorm(kv_a[:512]) (two bf16 roundings), k_pe = RoPE(kv_a[512:])
@@ -694,7 +704,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
                 kb = (uint16_t)bf16_bits(rope_one(L.u.s3.kva + kLora, cs_t, sn_t, tid));
                 L.u.s3.row[kLora + tid] = kb;
             }
-            if (h == 0) {
+            if (h3 == 0) {
                 uint16_t* crow = P.cache + (int64_t)pos * kRowElems;
                 crow[tid] = cb;
                 if (tid < kRope) crow[kLora + tid] = kb;
@@ -792,20 +802,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
             O = fma(L.u.s3.wf[w], L.u.s3.wo[w][tid], O);
             Ls = fma(L.u.s3.wf[w], L.u.s3.wl[w], Ls);
         }
-        publish_f64(ws->o_t[h][k][tid], O, tag);
+        publish_f64(ws->o_t[h3][k3][tid], O, tag);
         if (tid == 0) {
-            publish_f64(&ws->ml_t[h][k][0], M, tag);
-            publish_f64(&ws->ml_t[h][k][4], Ls, tag);
+            publish_f64(&ws->ml_t[h3][k3][0], M, tag);
+            publish_f64(&ws->ml_t[h3][k3][4], Ls, tag);
         }
     } else {
+        load_tail();
         // A chunk without positions (pos < 15) still publishes, a neutral
         // partial (max -inf, sums 0) that no merge reads: every polled word
         // is then rewritten on every call, so a word is never older than one
         // call and its 16-bit tag can never equal the current one by wrapping.
-        publish_f64(ws->o_t[h][k][tid], 0.0, tag);
+        publish_f64(ws->o_t[h3][k3][tid], 0.0, tag);
         if (tid == 0) {
-            publish_f64(&ws->ml_t[h][k][0], -INFINITY, tag);
-            publish_f64(&ws->ml_t[h][k][4], 0.0, tag);
+            publish_f64(&ws->ml_t[h3][k3][0], -INFINITY, tag);
+            publish_f64(&ws->ml_t[h3][k3][4], 0.0, tag);
         }
     }
     ATTN_TRACE(9);
