@@ -17,6 +17,16 @@
 
 namespace fleet_moe {
 
+// The workitem id, opaque to the compiler at each use: in the whole-step
+// kernel every stage derives its lane and wave indices afresh, instead of the
+// compiler hoisting them out of the layer loop and keeping them in registers
+// across every stage (which made that kernel spill).
+__device__ __forceinline__ int fm_tid() {
+    int t = (int)__builtin_amdgcn_workitem_id_x();
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // DeepSeek-V2-Lite MoE shape (reference/dsv2lite_config.json).
 constexpr int kHidden = 2048;
 constexpr int kInter = 1408;          // routed expert intermediate
@@ -213,7 +223,7 @@ __device__ __forceinline__ void nsum_level(float (&v)[N], int lane) {
 template <int N>
 __device__ __forceinline__ float wave_nsum(float (&v)[N]) {
     static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "N sums, N a power of 2 <= 16");
-    const int lane = threadIdx.x & 63;
+    const int lane = fm_tid() & 63;
     nsum_level<0>(v, lane);
     nsum_level<1>(v, lane);
     nsum_level<2>(v, lane);
@@ -308,7 +318,7 @@ __device__ __forceinline__ float msum_xchg(float x) {
         return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
     else
         return __int_as_float(__builtin_amdgcn_ds_bpermute(
-            (int)(((threadIdx.x & (kLanes - 1)) ^ 32u) << 2), __float_as_int(x)));
+            (int)(((fm_tid() & (kLanes - 1)) ^ 32u) << 2), __float_as_int(x)));
 }
 constexpr int kMsumDual[6] = {5, 6, 12, 8, 16, 32};
 
@@ -324,7 +334,7 @@ template <int K, int LEN, int N>
 __device__ __forceinline__ void msum_step(float (&v)[N]) {
     if constexpr (K < 6) {
         if constexpr (LEN > 1) {
-            const bool up = __builtin_popcount((threadIdx.x & (kLanes - 1)) & kMsumDual[K]) & 1;
+            const bool up = __builtin_popcount((fm_tid() & (kLanes - 1)) & kMsumDual[K]) & 1;
 #pragma unroll
             for (int j = 0; j < LEN / 2; ++j) {
                 const float lo = msum_pair<K>(v[j]);
@@ -377,7 +387,7 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ inline void wave_softmax_topk(float logit, int n, int k, float scaling,
                                          int* ids_out, float* w_out, const float* bias) {
-    const int lane = threadIdx.x & (kLanes - 1);
+    const int lane = fm_tid() & (kLanes - 1);
     const bool valid = lane < n;
     const float z = valid ? (bias ? logit + bias[lane] : logit) : -INFINITY;
     const float m = wave_max(z);
@@ -395,6 +405,42 @@ __device__ inline void wave_softmax_topk(float logit, int n, int k, float scalin
         }
         if (lane == sel) q = -INFINITY;
     }
+}
+
+// ---------------------------------------------------------------- residual exchange
+// The whole-step kernel (fleet_decode_step) hands the residual x (bf16-valued
+// fp32) from stage to stage as tagged words, tag | bf16 bits, in kXCopies
+// copies of kHidden words: every workgroup reads all of x (workgroup w polls
+// copy w % kXCopies, so each line sees 32 pollers instead of 256), and each
+// writer publishes its rows to every copy.
+constexpr int kXCopies = 8;
+
+// Polls this thread's four words x[4 tid .. 4 tid + 3] of the copy at `base`
+// (512 threads cover the 2048) until all four carry `tag`; returns them as
+// fp32. A wait that runs out sets `bit` in *abort and returns what it read.
+__device__ inline float4 poll_x4(const uint32_t* base, uint32_t tag, uint32_t* abort,
+                                 uint32_t bit) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(base);
+    for (uint32_t it = 0;; ++it) {
+        const u32x4 a = ld_dev16(r, 16 * (int)fm_tid());
+        const bool ok = ((a.x & 0xffff0000u) == tag) & ((a.y & 0xffff0000u) == tag) &
+                        ((a.z & 0xffff0000u) == tag) & ((a.w & 0xffff0000u) == tag);
+        const bool done = __all(ok);
+        if (done || it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(abort) != 0)) {
+            if (!done && (fm_tid() & (kLanes - 1)) == 0)
+                __hip_atomic_fetch_or(abort, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return make_float4(__uint_as_float(a.x << 16), __uint_as_float(a.y << 16),
+                               __uint_as_float(a.z << 16), __uint_as_float(a.w << 16));
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Row `row` of x (a bf16 value) into every copy at `xout`.
+__device__ __forceinline__ void publish_x(uint32_t* xout, int row, float v, uint32_t tag) {
+    const uint32_t w = tag | bf16_bits(v);
+#pragma unroll
+    for (int c = 0; c < kXCopies; ++c) st_agent(xout + c * kHidden + row, w);
 }
 
 }  // namespace fleet_moe

@@ -1,0 +1,272 @@
+// One greedy decode step of the whole model in ONE launch: embedding, every
+// decoder layer (the absorbed-MLA attention half, then the dense or MoE FFN
+// half), the final RMSNorm, lm_head and the argmax, with the token and the
+// position in device memory, so a decode loop is one launch per token (or one
+// graph node).
+//
+// The stages are the device code of the per-layer launches (attn_body.h,
+// moe_body.h, dense_body.h) run back to back by the same 256 workgroups (one
+// per CU, 8 waves each). What a launch boundary used to do between them is
+// done by the data itself: every stage publishes its residual rows as tagged
+// words (tag | bf16 bits) in an exchange buffer, and the next stage polls the
+// whole residual before it starts, so no workgroup runs ahead on a stale
+// input. Two exchange buffers alternate (attention outputs, FFN outputs).
+// Every stage's cross-workgroup words carry a call count unique to the
+// (step, layer), derived from the call counts read once at the start: the
+// attention, MoE and dense workspaces are reused by every layer, and a word a
+// stage polls is always rewritten by that stage, so it is at most one stage
+// old. Reuse is safe because every stage ends with an all-to-all exchange:
+// a workgroup can only write a stage's words after every workgroup has
+// published the previous stage's residual, which it does after its last read
+// of those words. Workgroup 0 advances the call counts at the very end, after
+// the argmax, which needed every workgroup's lm_head candidate.
+#include "attn_body.h"
+#include "dense_body.h"
+#include "moe_body.h"
+
+namespace fleet_moe {
+namespace step {
+
+constexpr int kWG = 256;
+constexpr int kThreads = 512;
+constexpr int kMaxLayers = 64;
+static_assert(attn::kWG == kWG && decode::kWG == kWG && dense::kWG == kWG, "one grid");
+static_assert(attn::kThreads == kThreads && decode::kThreads == kThreads &&
+                  dense::kThreads == kThreads,
+              "one workgroup shape");
+
+struct Workspace {
+    uint32_t epoch;                           // steps completed
+    uint32_t pad0;
+    uint32_t abort;                           // offset 8: sticky status
+    uint32_t pad1[61];
+    uint32_t x[2][kXCopies][kHidden];         // residual exchange: [0] attention, [1] FFN outputs
+};
+static_assert(offsetof(Workspace, abort) == 8, "status word offset");
+static_assert(offsetof(Workspace, x) % 16 == 0, "x is read with 16-byte loads");
+
+// Byte offsets of the four workspaces inside the caller's one buffer.
+constexpr size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+constexpr size_t kOffAttn = 0;
+constexpr size_t kOffMoe = kOffAttn + align256(sizeof(attn::Workspace));
+constexpr size_t kOffDense = kOffMoe + align256(sizeof(decode::Workspace));
+constexpr size_t kOffStep = kOffDense + align256(sizeof(dense::Workspace));
+constexpr size_t kBytes = kOffStep + align256(sizeof(Workspace));
+
+struct Params {
+    const fleet_step_layer* layers;   // device table
+    int32_t n_layers;
+    int32_t max_pos;
+    const uint16_t* embed;
+    const uint16_t* final_norm;
+    const uint16_t* lm_head;
+    const float* cos;
+    const float* sin;
+    const int32_t* token;
+    int32_t* token_out;
+    int32_t* token_next;
+    int32_t* pos_dev;
+    float* x_out;
+    float* logits;
+    double scale;
+    float eps;
+    float scaling;
+    attn::Workspace* aws;
+    decode::Workspace* mws;
+    dense::Workspace* dws;
+    Workspace* sws;
+};
+
+union Lds {
+    attn::Lds a;
+    decode::Lds m;
+    dense::Lds d;
+    attn::HeadLds h;
+};
+
+__global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
+    __shared__ Lds L;
+    const int wg = blockIdx.x, tid = threadIdx.x;
+    const int pos = *S.pos_dev;
+    const int token = *S.token;
+    if (pos < 0 || pos >= S.max_pos || token < 0 || token >= attn::kVocab) {
+        if (wg == 0 && tid == 0)
+            attn::raise(S.aws, (pos < 0 || pos >= S.max_pos) ? FLEET_MOE_ABORT_POSITION
+                                                             : FLEET_MOE_ABORT_TOKEN);
+        return;
+    }
+    // the call counts, written by the previous launch (plain loads: current
+    // after the launch boundary)
+    const uint32_t ea = S.aws->epoch, em = S.mws->epoch, ed = S.dws->epoch, es = S.sws->epoch;
+    // exchange tags: 64 per step (2 per layer), so consecutive steps differ
+    const uint32_t sbase = (es + 1u) * 64u;
+    auto xtag = [&](int stage) { return ((sbase + (uint32_t)stage) & 0xffffu) << 16; };
+    uint32_t* xa = &S.sws->x[0][0][0];
+    uint32_t* xf = &S.sws->x[1][0][0];
+    int n_moe = 0, n_dense = 0;
+    for (int i = 0; i < S.n_layers; ++i) {
+        const fleet_step_layer& ly = S.layers[i];
+        const bool last = i == S.n_layers - 1;
+        {
+            attn::Params A{};
+            A.norm_in = ly.attn.norm_in;
+            A.qkv = ly.attn.qkv;
+            A.kv_a_norm = ly.attn.kv_a_norm;
+            A.kv_b = ly.attn.kv_b;
+            A.o_proj = ly.attn.o_proj;
+            A.cache = ly.cache;
+            A.cos = S.cos;
+            A.sin = S.sin;
+            A.pos_host = pos;
+            A.max_pos = S.max_pos;
+            A.scale = S.scale;
+            A.eps = S.eps;
+            A.ws = S.aws;
+            A.epoch = ea + 1u + (uint32_t)i;
+            A.xin = i == 0 ? nullptr : xf;
+            A.xin_row = i == 0 ? S.embed + (int64_t)token * kHidden : nullptr;
+            A.xin_tag = xtag(2 * i);
+            A.xout = xa;
+            A.xout_tag = xtag(2 * i + 1);
+            attn::attn_layer<true>(A, L.a);
+        }
+        __syncthreads();
+        if (ly.dense) {
+            dense::Params D{};
+            D.norm = ly.moe.norm;
+            D.w = ly.dense;
+            D.x_out = last ? S.x_out : nullptr;
+            D.ws = S.dws;
+            D.eps = S.eps;
+            D.epoch = ed + 1u + (uint32_t)n_dense++;
+            D.xin = xa;
+            D.xin_tag = xtag(2 * i + 1);
+            D.xout = xf;
+            D.xout_tag = xtag(2 * i + 2);
+            dense::dense_layer<true>(D, L.d);
+        } else {
+            decode::Params M{};
+            M.norm = ly.moe.norm;
+            M.router = reinterpret_cast<const u32x4*>(ly.moe.router);
+            M.experts = ly.moe.experts;
+            M.shared = ly.moe.shared;
+            M.x_out = last ? S.x_out : nullptr;
+            M.ws = S.mws;
+            M.expert_stride = ly.moe.expert_stride;
+            M.eps = S.eps;
+            M.scaling = S.scaling;
+            M.epoch = em + 1u + (uint32_t)n_moe++;
+            M.xin = xa;
+            M.xin_tag = xtag(2 * i + 1);
+            M.xout = xf;
+            M.xout_tag = xtag(2 * i + 2);
+            decode::moe_layer<true>(M, L.m);
+        }
+        __syncthreads();
+    }
+    {
+        attn::HeadParams H{};
+        H.norm = S.final_norm;
+        H.W = S.lm_head;
+        H.eps = S.eps;
+        H.logits = S.logits;
+        H.ws = S.aws;
+        H.xin = xf;
+        H.xin_tag = xtag(2 * S.n_layers);
+        H.epoch = es + 1u;
+        H.token_out = S.token_out;
+        H.token_next = S.token_next;
+        H.pos_advance = S.pos_dev;
+        attn::lmhead_body<true>(H, L.h);
+    }
+    if (wg == 0 && tid == 0) {
+        st_agent(&S.aws->epoch, ea + (uint32_t)S.n_layers);
+        st_agent(&S.mws->epoch, em + (uint32_t)n_moe);
+        st_agent(&S.dws->epoch, ed + (uint32_t)n_dense);
+        st_agent(&S.sws->epoch, es + 1u);
+    }
+}
+
+}  // namespace step
+}  // namespace fleet_moe
+
+using namespace fleet_moe;
+
+int fleet_moe_check_dims(const fleet_moe_dims* d);
+int fleet_moe_check_resident(const void* fn, int threads, int grid);
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+extern "C" size_t fleet_decode_step_workspace_bytes(const fleet_moe_dims* dims) {
+    if (!dims || fleet_moe_check_dims(dims) != 0) return 0;
+    return step::kBytes;
+}
+
+extern "C" int fleet_decode_step(const fleet_step_model* model, const int32_t* token,
+                                 int32_t* token_out, int32_t* token_next, int32_t* pos_dev,
+                                 float* x_out, float* logits, void* workspace,
+                                 size_t workspace_bytes, const fleet_moe_dims* dims,
+                                 hipStream_t stream) {
+    if (!model || !dims) return FLEET_MOE_ERR_ARG;
+    if (int e = fleet_moe_check_dims(dims)) return e;
+    if (!model->layers || model->n_layers < 1 || model->n_layers > step::kMaxLayers ||
+        !model->embed || !model->lm_head || !model->rope_cos || !model->rope_sin ||
+        model->max_pos < 1 || model->max_pos > attn::kMaxPos || !token || !pos_dev ||
+        !workspace)
+        return FLEET_MOE_ERR_ARG;
+    if (!aligned(model->layers, 8) || !aligned(model->embed, 16) || !aligned(model->lm_head, 16) ||
+        (model->final_norm && !aligned(model->final_norm, 8)) || !aligned(model->rope_cos, 4) ||
+        !aligned(model->rope_sin, 4) || !aligned(token, 4) || !aligned(pos_dev, 4) ||
+        (token_out && !aligned(token_out, 4)) || (token_next && !aligned(token_next, 4)) ||
+        (x_out && !aligned(x_out, 4)) || (logits && !aligned(logits, 4)) ||
+        !aligned(workspace, 256))
+        return FLEET_MOE_ERR_ARG;
+    if (workspace_bytes < step::kBytes) return FLEET_MOE_ERR_WORKSPACE;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&step::step_kernel),
+                                         step::kThreads, step::kWG))
+        return e;
+    uint8_t* w = static_cast<uint8_t*>(workspace);
+    step::Params S{};
+    S.layers = model->layers;
+    S.n_layers = model->n_layers;
+    S.max_pos = model->max_pos;
+    S.embed = model->embed;
+    S.final_norm = model->final_norm;
+    S.lm_head = model->lm_head;
+    S.cos = model->rope_cos;
+    S.sin = model->rope_sin;
+    S.token = token;
+    S.token_out = token_out;
+    S.token_next = token_next;
+    S.pos_dev = pos_dev;
+    S.x_out = x_out;
+    S.logits = logits;
+    // (qk_nope + qk_rope)^-0.5 * mscale(40, 0.707)^2 (src/host/reference_decode.py:
+    // 78-83, 197-203), in double
+    const double m = 0.1 * 0.707 * std::log(40.0) + 1.0;
+    S.scale = std::pow(192.0, -0.5) * m * m;
+    S.eps = dims->rms_eps;
+    S.scaling = dims->routed_scaling;
+    S.aws = reinterpret_cast<attn::Workspace*>(w + step::kOffAttn);
+    S.mws = reinterpret_cast<decode::Workspace*>(w + step::kOffMoe);
+    S.dws = reinterpret_cast<dense::Workspace*>(w + step::kOffDense);
+    S.sws = reinterpret_cast<step::Workspace*>(w + step::kOffStep);
+    hipLaunchKernelGGL(step::step_kernel, dim3(step::kWG), dim3(step::kThreads), 0, stream, S);
+    return (int)hipGetLastError();
+}
+
+extern "C" int fleet_decode_step_status(const void* workspace, uint32_t* status,
+                                        hipStream_t stream) {
+    if (!workspace || !status || !aligned(workspace, 256)) return FLEET_MOE_ERR_ARG;
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    const size_t offs[4] = {step::kOffAttn, step::kOffMoe, step::kOffDense, step::kOffStep};
+    const char* w = static_cast<const char*>(workspace);
+    for (int i = 0; i < 4; ++i) {
+        hipError_t e = hipMemcpyAsync(&v[i], w + offs[i] + 8, sizeof(uint32_t),
+                                      hipMemcpyDeviceToHost, stream);
+        if (e != hipSuccess) return (int)e;
+    }
+    if (hipError_t e = hipStreamSynchronize(stream)) return (int)e;
+    *status = v[0] | v[1] | v[2] | v[3];
+    return 0;
+}

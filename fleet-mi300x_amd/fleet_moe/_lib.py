@@ -28,6 +28,7 @@ ABORT_POSITION = 0x8
 ABORT_TOKEN = 0x10
 ABORT_ATTN_WAIT = 0x20
 ABORT_BAD_ID = 0x40
+ABORT_STEP_WAIT = 0x80
 
 
 class FleetMoeDims(ctypes.Structure):
@@ -47,6 +48,19 @@ class FleetAttnLayer(ctypes.Structure):
     """struct fleet_attn_layer (device pointers)."""
     _fields_ = [("norm_in", c_void_p), ("qkv", c_void_p), ("kv_a_norm", c_void_p),
                 ("kv_b", c_void_p), ("o_proj", c_void_p)]
+
+
+class FleetStepLayer(ctypes.Structure):
+    """struct fleet_step_layer (device pointers)."""
+    _fields_ = [("attn", FleetAttnLayer), ("moe", FleetMoeLayer), ("dense", c_void_p),
+                ("cache", c_void_p)]
+
+
+class FleetStepModel(ctypes.Structure):
+    """struct fleet_step_model (layers: a device array of FleetStepLayer)."""
+    _fields_ = [("layers", c_void_p), ("n_layers", c_int32), ("max_pos", c_int32),
+                ("embed", c_void_p), ("final_norm", c_void_p), ("lm_head", c_void_p),
+                ("rope_cos", c_void_p), ("rope_sin", c_void_p)]
 
 
 # (name, restype, argtypes) of every symbol the header declares.
@@ -75,6 +89,11 @@ SYMBOLS = [
     ("fleet_attn_decode", c_int,
      [POINTER(FleetAttnLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
       c_void_p, c_void_p, c_void_p, c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_decode_step_workspace_bytes", c_size_t, [POINTER(FleetMoeDims)]),
+    ("fleet_decode_step", c_int,
+     [POINTER(FleetStepModel), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+      c_void_p, c_size_t, POINTER(FleetMoeDims), c_void_p]),
+    ("fleet_decode_step_status", c_int, [c_void_p, POINTER(ctypes.c_uint32), c_void_p]),
     ("fleet_embed", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("fleet_lm_head_argmax", c_int,
      [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -330,10 +330,14 @@ class Decoder:
     token = argmax(bf16(lm_head . rms_norm(x))). The KV cache is
     [layers][max_pos][576] bf16. The token and the position live in device
     memory (`token`, `pos`), so one step can be captured in a HIP graph and
-    replayed: the argmax writes the next token and advances the position."""
+    replayed: the argmax writes the next token and advances the position.
+    With `fused` (the default) a step is ONE launch (fleet_decode_step) that
+    runs all of it; otherwise one launch per stage (embed, per layer
+    attention and FFN, lm_head, argmax). The results are the same bit for
+    bit."""
 
     def __init__(self, blob: torch.Tensor, layout: Layout, dims: MoeDims = DSV2_LITE,
-                 max_pos: int = 4096):
+                 max_pos: int = 4096, fused: bool = True):
         from .rope import RopeParams, yarn_tables
         self.blob, self.layout, self.dims = blob, layout, dims
         dev = blob.device
@@ -352,6 +356,9 @@ class Decoder:
         self.token_out = torch.zeros(1, dtype=torch.int32, device=dev)  # last pick
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)        # position of the next step
         self.graph = None
+        self.fused = bool(fused)
+        if self.fused:
+            self._init_step()
 
     def _addr(self, name: str) -> int:
         return self.blob.data_ptr() + self.layout.tensors[name].offset
@@ -368,11 +375,44 @@ class Decoder:
                             self.pos if use_pos_dev else None, self.cos, self.sin, stream)
         self.ffn.layer_into(i, x, x, stream)
 
+    def _init_step(self) -> None:
+        """The device layer table and the workspace of fleet_decode_step."""
+        lib = _lib.load()
+        rows = (_lib.FleetStepLayer * self.n_layers)()
+        for i in range(self.n_layers):
+            r = rows[i]
+            r.attn = self.attn_layers[i]
+            r.cache = self.cache[i].data_ptr()
+            if i < self.ffn.first_k_dense:
+                r.moe = _lib.FleetMoeLayer(self._addr(f"L{i}.norm_post"), None, None, 0, None)
+                r.dense = self._addr(f"L{i}.dense")
+            else:
+                r.moe = self.ffn.moe[i].c_layer()
+                r.dense = None
+        raw = bytes(memoryview(rows).cast("B"))
+        self.step_layers = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.blob.device)
+        self.step_model = _lib.FleetStepModel(
+            self.step_layers.data_ptr(), self.n_layers, self.max_pos, self._addr("embed"),
+            self._addr("final_norm") if "final_norm" in self.layout.tensors else None,
+            self._addr("lm_head"), self.cos.data_ptr(), self.sin.data_ptr())
+        n = lib.fleet_decode_step_workspace_bytes(ctypes.byref(self.attn._dims))
+        if n == 0:
+            raise ValueError("fleet_decode_step does not support these model dims")
+        self.step_ws = torch.zeros(n, dtype=torch.uint8, device=self.blob.device)
+
     def enqueue_step(self, logits: torch.Tensor | None = None, feed_back: bool = True,
                      stream=None) -> None:
         """One token from device state: embed(*token), every layer at *pos,
         lm_head + argmax -> token_out (and -> token when feed_back), *pos += 1.
         No allocation, no synchronisation: capturable."""
+        if self.fused:
+            rc = _lib.load().fleet_decode_step(
+                ctypes.byref(self.step_model), _ptr(self.token), _ptr(self.token_out),
+                _ptr(self.token) if feed_back else None, _ptr(self.pos), _ptr(self.x),
+                _ptr(logits), _ptr(self.step_ws), self.step_ws.numel(),
+                ctypes.byref(self.attn._dims), _stream(stream))
+            _lib.check(rc, "fleet_decode_step")
+            return
         self.attn.embed_into(self._addr("embed"), self.token, self.x, stream)
         for i in range(self.n_layers):
             self.layer_into(i, self.x, use_pos_dev=True, stream=stream)
@@ -420,4 +460,10 @@ class Decoder:
         return out
 
     def status(self) -> int:
-        return self.attn.status() | self.ffn.status()
+        st = self.attn.status() | self.ffn.status()
+        if self.fused:
+            v = ctypes.c_uint32(0)
+            _lib.check(_lib.load().fleet_decode_step_status(_ptr(self.step_ws), ctypes.byref(v),
+                                                            None), "fleet_decode_step_status")
+            st |= int(v.value)
+        return st

@@ -230,6 +230,63 @@ int fleet_attn_decode(const fleet_attn_layer* layer, const float* x, float* x_ou
                       const float* rope_cos, const float* rope_sin, void* workspace,
                       size_t workspace_bytes, const fleet_moe_dims* dims, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * The whole decode step in one launch (no separate counterpart in the
+ * reference, whose persistent kernel runs a step's task graph in one launch:
+ * src/kernels/fleet_kernel.hip:933-1040, driven by src/host/fleet_launch.hip).
+ * Same arithmetic as embed, then per layer fleet_attn_decode and
+ * fleet_moe_dense_decode / fleet_moe_layer_decode, then fleet_lm_head_argmax:
+ * every result equals that sequence's bit for bit. */
+
+/* One decoder layer: its attention weights, its FFN (the dense SwiGLU blob
+ * "L{i}.dense" when dense is not NULL, with moe.norm as its post-attention
+ * norm and the other moe fields unused; else the MoE layer moe) and its KV
+ * cache (bf16 [max_pos][576]). */
+typedef struct fleet_step_layer {
+    fleet_attn_layer attn;
+    fleet_moe_layer moe;
+    const uint16_t* dense;
+    uint16_t* cache;
+} fleet_step_layer;
+
+/* The model: layers is a DEVICE array of n_layers (<= 64) entries, which the
+ * kernel reads; embed, lm_head bf16 [102400][hidden]; final_norm bf16[hidden]
+ * or NULL; rope_cos / rope_sin fp32 [max_pos][64], max_pos <= 4096. */
+typedef struct fleet_step_model {
+    const fleet_step_layer* layers;
+    int32_t n_layers;
+    int32_t max_pos;
+    const uint16_t* embed;
+    const uint16_t* final_norm;
+    const uint16_t* lm_head;
+    const float* rope_cos;
+    const float* rope_sin;
+} fleet_step_model;
+
+/* Workspace bytes fleet_decode_step needs (one buffer; about 2.8 MB). */
+size_t fleet_decode_step_workspace_bytes(const fleet_moe_dims* dims);
+
+/* One greedy step at position *pos_dev for the token *token (device int32s):
+ * x = embed[token], every layer (attention half, then FFN half), then
+ * token = argmax(bf16(lm_head . rms_norm(x, final_norm))) (lowest index on
+ * ties) into *token_out and *token_next (either may be NULL; token_next may
+ * equal token, feeding the next step), and *pos_dev += 1. x_out: fp32[hidden]
+ * receives the final residual, or NULL; logits: fp32[102400] or NULL. One
+ * launch of 256 workgroups (one per CU), all resident at once (checked as for
+ * fleet_moe_layer_decode). A position outside [0, max_pos) or a token outside
+ * the vocabulary sets FLEET_MOE_ABORT_POSITION / _TOKEN and the step does
+ * nothing else; a stage whose input never arrives sets
+ * FLEET_MOE_ABORT_STEP_WAIT (or its stage's wait bit). Calls on one workspace
+ * must be ordered on one stream. */
+int fleet_decode_step(const fleet_step_model* model, const int32_t* token, int32_t* token_out,
+                      int32_t* token_next, int32_t* pos_dev, float* x_out, float* logits,
+                      void* workspace, size_t workspace_bytes, const fleet_moe_dims* dims,
+                      hipStream_t stream);
+
+/* The FLEET_MOE_ABORT_* bits recorded in a fleet_decode_step workspace (the
+ * OR over its stages), read synchronously on `stream`. */
+int fleet_decode_step_status(const void* workspace, uint32_t* status, hipStream_t stream);
+
 /* x = embed[*token] as fp32 (the EMBED task, src/kernels/fleet_kernel.hip:
  * 68-78). token: a device int32, so a decode loop can feed the previous
  * step's argmax without a host round trip; a token outside [0, 102400) sets
@@ -265,6 +322,8 @@ int fleet_moe_workspace_status(const void* workspace, uint32_t* status, hipStrea
 #define FLEET_MOE_ABORT_ATTN_WAIT 0x20u   /* an attention stage never completed */
 #define FLEET_MOE_ABORT_BAD_ID 0x40u      /* grouped: an expert id outside [0, n_routed)
                                              was clamped into range (output unspecified) */
+#define FLEET_MOE_ABORT_STEP_WAIT 0x80u   /* fleet_decode_step: a stage's input residual
+                                             (or an lm_head candidate) never arrived */
 
 /* Diagnostic: reads `bytes` of device memory with the weight-streaming load
  * pattern of the kernels above (16-byte non-temporal loads, 1 KB per wave
