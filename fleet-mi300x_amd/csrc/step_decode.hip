@@ -24,6 +24,10 @@
 #include "dense_body.h"
 #include "moe_body.h"
 
+#ifndef FLEET_STEP_TRACE
+#define FLEET_STEP_TRACE 0
+#endif
+
 namespace fleet_moe {
 namespace step {
 
@@ -75,6 +79,12 @@ struct Params {
     decode::Workspace* mws;
     dense::Workspace* dws;
     Workspace* sws;
+#if FLEET_STEP_TRACE
+    unsigned long long* trace;     // [2 n_layers + 2][kWG] stage-end stamps, or null
+    unsigned long long* trace_a;   // the attention stage trace of layer trace_layer
+    unsigned long long* trace_m;   // its FFN stage trace
+    int trace_layer;
+#endif
 };
 
 union Lds {
@@ -104,6 +114,13 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     uint32_t* xa = &S.sws->x[0][0][0];
     uint32_t* xf = &S.sws->x[1][0][0];
     int n_moe = 0, n_dense = 0;
+#if FLEET_STEP_TRACE
+#define STEP_TRACE(k) \
+    do { if (S.trace && tid == 0) S.trace[(size_t)(k) * kWG + wg] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define STEP_TRACE(k) do {} while (0)
+#endif
+    STEP_TRACE(0);
     for (int i = 0; i < S.n_layers; ++i) {
         const fleet_step_layer& ly = S.layers[i];
         const bool last = i == S.n_layers - 1;
@@ -128,9 +145,13 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             A.xin_tag = xtag(2 * i);
             A.xout = xa;
             A.xout_tag = xtag(2 * i + 1);
+#if FLEET_STEP_TRACE && FLEET_ATTN_TRACE
+            A.trace = i == S.trace_layer ? S.trace_a : nullptr;
+#endif
             attn::attn_layer<true>(A, L.a);
         }
         __syncthreads();
+        STEP_TRACE(1 + 2 * i);
         if (ly.dense) {
             dense::Params D{};
             D.norm = ly.moe.norm;
@@ -160,9 +181,13 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             M.xin_tag = xtag(2 * i + 1);
             M.xout = xf;
             M.xout_tag = xtag(2 * i + 2);
+#if FLEET_STEP_TRACE && FLEET_MOE_TRACE
+            M.trace = i == S.trace_layer ? S.trace_m : nullptr;
+#endif
             decode::moe_layer<true>(M, L.m);
         }
         __syncthreads();
+        STEP_TRACE(2 + 2 * i);
     }
     {
         attn::HeadParams H{};
@@ -179,6 +204,7 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
         H.pos_advance = S.pos_dev;
         attn::lmhead_body<true>(H, L.h);
     }
+    STEP_TRACE(2 * S.n_layers + 1);
     if (wg == 0 && tid == 0) {
         st_agent(&S.aws->epoch, ea + (uint32_t)S.n_layers);
         st_agent(&S.mws->epoch, em + (uint32_t)n_moe);
@@ -196,6 +222,17 @@ int fleet_moe_check_dims(const fleet_moe_dims* d);
 int fleet_moe_check_resident(const void* fn, int threads, int grid);
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+#if FLEET_STEP_TRACE
+static unsigned long long *g_step_trace, *g_step_trace_a, *g_step_trace_m;
+static int g_step_trace_layer = -1;
+extern "C" void fleet_step_debug_set_trace(void* t, void* a, void* m, int layer) {
+    g_step_trace = (unsigned long long*)t;
+    g_step_trace_a = (unsigned long long*)a;
+    g_step_trace_m = (unsigned long long*)m;
+    g_step_trace_layer = layer;
+}
+#endif
 
 extern "C" size_t fleet_decode_step_workspace_bytes(const fleet_moe_dims* dims) {
     if (!dims || fleet_moe_check_dims(dims) != 0) return 0;
@@ -251,6 +288,12 @@ extern "C" int fleet_decode_step(const fleet_step_model* model, const int32_t* t
     S.mws = reinterpret_cast<decode::Workspace*>(w + step::kOffMoe);
     S.dws = reinterpret_cast<dense::Workspace*>(w + step::kOffDense);
     S.sws = reinterpret_cast<step::Workspace*>(w + step::kOffStep);
+#if FLEET_STEP_TRACE
+    S.trace = g_step_trace;
+    S.trace_a = g_step_trace_a;
+    S.trace_m = g_step_trace_m;
+    S.trace_layer = g_step_trace_layer;
+#endif
     hipLaunchKernelGGL(step::step_kernel, dim3(step::kWG), dim3(step::kThreads), 0, stream, S);
     return (int)hipGetLastError();
 }

@@ -1,7 +1,8 @@
 """In-tree build of libfleet_moe.so for gfx950 with hipcc.
 
-Every HIP source under ../csrc is compiled into one shared library next to
-this file. Runs on a machine without a GPU (hipcc cross-compiles gfx950).
+Every HIP source under ../csrc is compiled to an object (in parallel) and the
+objects are linked into one shared library next to this file. Runs on a machine without a GPU (hipcc
+cross-compiles gfx950).
 """
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ INCLUDE = PKG.parents[1] / "include"
 OUT = PKG / "libfleet_moe.so"
 
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # keep the compiler from emitting packed fp32 arithmetic
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
@@ -34,20 +35,38 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source into OUT (always recompiles). Returns the path."""
-    tmp = OUT.with_name(OUT.name + ".tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(tmp),
-           *map(str, sources())]
+def _run(cmd: list[str], verbose: bool) -> subprocess.Popen:
     if verbose:
         print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _check(p: subprocess.Popen, what: str, verbose: bool) -> None:
+    out, _ = p.communicate()
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
+    err = "\n".join(l for l in out.splitlines() if noise not in l)
+    if p.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {what} ({p.returncode}):\n{err}")
     if verbose and err.strip():
         print(err)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source into OUT (always recompiles). Returns the path."""
+    objdir = PKG / "_obj"
+    objdir.mkdir(exist_ok=True)
+    jobs, objs = [], []
+    for src in sources():
+        obj = objdir / (src.stem + ".o")
+        cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", "-o", str(obj),
+               str(src)]
+        jobs.append((_run(cmd, verbose), src.name))
+        objs.append(obj)
+    for p, name in jobs:
+        _check(p, name, verbose)
+    tmp = OUT.with_name(OUT.name + ".tmp")
+    link = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    _check(_run(link, verbose), "the link", verbose)
     os.replace(tmp, OUT)
     return OUT
 
