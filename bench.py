@@ -437,7 +437,10 @@ def bench_decode(torch, dev, stream, dims, prompt_len: int = 1024, n_gen: int = 
     device. The KV cache is prefilled by teacher-forced steps over a seeded
     uniform prompt of 1024 tokens, then 32 greedy tokens are generated; each
     step is one replay of the captured HIP graph of the step (the token and
-    the position live on the device, the argmax feeds both forward)."""
+    the position live on the device, the argmax feeds both forward). The step
+    is one launch (fleet_decode_step); the same 32 tokens are also timed with
+    one launch per stage (embed, per layer attention and FFN, lm_head,
+    argmax) for comparison."""
     from fleet_moe import layout as lay_mod, ops, synth_gpu
     lay = lay_mod.model_layout(dims, n_layers=27)
     blob = torch.empty(lay.nbytes, dtype=torch.uint8, device=dev)
@@ -478,6 +481,25 @@ def bench_decode(torch, dev, stream, dims, prompt_len: int = 1024, n_gen: int = 
     d.record(stream)
     torch.cuda.synchronize()
     ms_tok_eager = c.elapsed_time(d) / n_gen
+    # the same steps as separate launches per stage (graph of ~56 launches)
+    sep = ops.Decoder(blob, lay, dims, max_pos=max_pos, fused=False)
+    sep.cache.copy_(dec.cache)
+    sep.capture()
+    sep.token.copy_(prompt_d[-1:])
+    sep.pos.fill_(prompt_len - 1)
+    sep.step()
+    toks_s = torch.empty_like(toks)
+    e = torch.cuda.Event(enable_timing=True)
+    f = torch.cuda.Event(enable_timing=True)
+    e.record(stream)
+    for j in range(n_gen):
+        sep.graph.replay()
+        toks_s[j:j + 1].copy_(sep.token_out)
+    f.record(stream)
+    torch.cuda.synchronize()
+    ms_tok_sep = e.elapsed_time(f) / n_gen
+    sep_status = sep.status()
+    del sep
     H = dims.hidden
     attn_bytes = (lay_mod.QKV_ROWS * H + lay_mod.ATTN_HEADS * (lay_mod.QK_NOPE + lay_mod.V_HEAD)
                   * lay_mod.KV_LORA + H * lay_mod.ATTN_HEADS * lay_mod.V_HEAD) * 2
@@ -490,16 +512,19 @@ def bench_decode(torch, dev, stream, dims, prompt_len: int = 1024, n_gen: int = 
     out = {
         "workload": "27-layer DeepSeek-V2-Lite-shape decode, batch 1, absorbed MLA, "
                     f"KV cache prefilled with {prompt_len} seeded uniform tokens, {n_gen} greedy "
-                    "tokens, weights N(0,0.02^2) bf16 drawn on the device (BASELINE config 4)",
+                    "tokens, weights N(0,0.02^2) bf16 drawn on the device, one launch per "
+                    "token (BASELINE config 4)",
         "ms_per_token": round(ms_tok, 4), "tokens_per_s": round(1e3 / ms_tok, 1),
         "ms_per_token_eager": round(ms_tok_eager, 4),
+        "ms_per_token_separate_launches": round(ms_tok_sep, 4),
         "bytes_per_token": tok_bytes,
         "hbm_gbs": round(tok_bytes / (ms_tok * 1e-3) / 1e9, 1),
         "hbm_frac": round(tok_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "prefill_s": round(prefill_s, 3),
         "graph_equals_eager": bool(torch.equal(toks, toks_e)),
+        "fused_equals_separate": bool(torch.equal(toks, toks_s)),
         "tokens_head": [int(t) for t in toks[:8].cpu()],
-        "status": dec.status(),
+        "status": dec.status() | sep_status,
     }
     del dec, blob
     torch.cuda.empty_cache()

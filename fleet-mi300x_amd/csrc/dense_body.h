@@ -22,7 +22,8 @@
 //             8w + r (21,888 B) into registers, then the workgroup polls the
 //             10944 h words once into LDS (bf16) and every wave takes its dot.
 // Every wait is bounded and records FLEET_MOE_ABORT_UNIT_WAIT instead of
-// hanging; the last workgroup to exit advances the epoch.
+// hanging; workgroup 0 advances the call count once it has seen every
+// workgroup's h.
 #pragma once
 #include <stddef.h>
 

@@ -46,7 +46,8 @@
 // 64-bit word (epoch << 32 | fp32 bits), written and read with device-scope
 // (sc1) accesses. A consumer polls the words it needs until every tag equals
 // the current call's epoch: no flags, no release fences, no L2 write-backs.
-// The last workgroup to exit advances the epoch. Every wait is bounded and
+// Workgroup 0 advances the call count once it has seen every workgroup's
+// tagged h. Every wait is bounded and
 // records an abort reason instead of hanging.
 #pragma once
 #include <stddef.h>
