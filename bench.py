@@ -376,8 +376,9 @@ def bench_cold(torch, dev, stream, dims, x_host, gx_host, lib, bytes_layer, no_g
 
 def bench_column(torch, dev, stream, dims, n_tok: int = 32, warm: int = 4):
     """Config 3: the FFN half of all 27 layers (dense layer 0 + 26 MoE layers)
-    chained at batch 1 over 32 seeded tokens, weights drawn on the device.
-    Also times the dense layer alone (its own roofline)."""
+    chained at batch 1 over 32 seeded tokens, weights drawn on the device, one
+    launch per token (fleet_ffn_column); the same tokens also with one launch
+    per layer. Also times the dense layer alone (its own roofline)."""
     from fleet_moe import layout as lay_mod, ops, synth, synth_gpu
     lay = lay_mod.column_layout(dims, n_layers=27)
     blob = torch.empty(lay.nbytes, dtype=torch.uint8, device=dev)
@@ -398,6 +399,19 @@ def bench_column(torch, dev, stream, dims, n_tok: int = 32, warm: int = 4):
     b.record(stream)
     torch.cuda.synchronize()
     us_tok = a.elapsed_time(b) * 1e3 / n_tok
+    # the same tokens with one launch per layer
+    col.fused = False
+    for t in range(warm):
+        col.run_into(xd[t], stream)
+    a2 = torch.cuda.Event(enable_timing=True)
+    b2 = torch.cuda.Event(enable_timing=True)
+    a2.record(stream)
+    for t in range(warm, warm + n_tok):
+        col.run_into(xd[t], stream)
+    b2.record(stream)
+    torch.cuda.synchronize()
+    us_tok_sep = a2.elapsed_time(b2) * 1e3 / n_tok
+    col.fused = True
     # dense layer 0 alone, back to back
     y = torch.empty_like(xd[0])
     nd = 50
@@ -415,9 +429,10 @@ def bench_column(torch, dev, stream, dims, n_tok: int = 32, warm: int = 4):
     status = col.status()
     out = {
         "workload": "27-layer FFN column (dense layer 0 + 26 MoE layers), batch 1, "
-                    f"{n_tok} chained tokens, weights N(0,0.02^2) bf16 drawn on the device "
-                    "(BASELINE config 3)",
+                    f"{n_tok} chained tokens, weights N(0,0.02^2) bf16 drawn on the device, "
+                    "one launch per token (BASELINE config 3)",
         "us_per_token": round(us_tok, 1), "tokens_per_s": round(1e6 / us_tok, 1),
+        "us_per_token_separate_launches": round(us_tok_sep, 1),
         "bytes_per_token": tok_bytes,
         "hbm_gbs": round(tok_bytes / (us_tok * 1e-6) / 1e9, 1),
         "hbm_frac": round(tok_bytes / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),

@@ -63,7 +63,8 @@ struct Params {
     float eps;
     // the whole-step kernel only
     uint32_t epoch;            // this layer's call count
-    const uint32_t* xin;       // tagged x [kXCopies][kHidden]
+    const uint32_t* xin;       // tagged x [kXCopies][kHidden], or null: xin_f32
+    const float* xin_f32;      // x itself (the first stage of a launch)
     uint32_t xin_tag;
     uint32_t* xout;            // tagged x_out [kXCopies][kHidden]
     uint32_t xout_tag;
@@ -115,9 +116,13 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L) {
     if (cur >= 0) issue_pair(gu + (int64_t)(wg + kWG * cur) * 2 * kRowChunks, lane, buf);
     if (tid == 0) L.next = kWaves;
     if constexpr (kMega) {
-        // x: every workgroup's published rows (polled behind this wave's first pair)
-        xv = poll_x4(P.xin + (wg % kXCopies) * kHidden, P.xin_tag, &ws->abort,
-                     FLEET_MOE_ABORT_STEP_WAIT);
+        // x: every workgroup's published rows (polled behind this wave's first
+        // pair), or the launch's input vector
+        if (P.xin_f32)
+            xv = reinterpret_cast<const float4*>(P.xin_f32)[tid];
+        else
+            xv = poll_x4(P.xin + (wg % kXCopies) * kHidden, P.xin_tag, &ws->abort,
+                         FLEET_MOE_ABORT_STEP_WAIT);
         reinterpret_cast<float4*>(L.xraw)[tid] = xv;
     }
 

@@ -119,7 +119,8 @@ struct Params {
     float scaling;
     // the whole-step kernel only
     uint32_t epoch;            // this layer's call count
-    const uint32_t* xin;       // tagged x [kXCopies][kHidden]
+    const uint32_t* xin;       // tagged x [kXCopies][kHidden], or null: xin_f32
+    const float* xin_f32;      // x itself (the first stage of a launch)
     uint32_t xin_tag;
     uint32_t* xout;            // tagged x_out [kXCopies][kHidden]
     uint32_t xout_tag;
@@ -491,9 +492,13 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
     if (tid < 8) { L.ids[tid] = 0; L.w[tid] = 0.f; L.order[tid] = tid; }
     if constexpr (kMega) {
         // x: every workgroup's published rows (polled behind this wave's first
-        // router rows and pair, which are in flight already)
-        xv = poll_x4(P.xin + (wg % kXCopies) * kHidden, P.xin_tag, &ws->abort,
-                     FLEET_MOE_ABORT_STEP_WAIT);
+        // router rows and pair, which are in flight already), or the launch's
+        // input vector
+        if (P.xin_f32)
+            xv = reinterpret_cast<const float4*>(P.xin_f32)[tid];
+        else
+            xv = poll_x4(P.xin + (wg % kXCopies) * kHidden, P.xin_tag, &ws->abort,
+                         FLEET_MOE_ABORT_STEP_WAIT);
         reinterpret_cast<float4*>(L.xraw)[tid] = xv;
     }
 

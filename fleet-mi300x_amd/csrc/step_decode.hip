@@ -70,6 +70,7 @@ struct Params {
     int32_t* token_out;
     int32_t* token_next;
     int32_t* pos_dev;
+    const float* x_in;         // the FFN column's input (kFull false)
     float* x_out;
     float* logits;
     double scale;
@@ -94,25 +95,32 @@ union Lds {
     attn::HeadLds h;
 };
 
+// kFull: the decode step (embed, attention and FFN of every layer, lm_head,
+// argmax). Otherwise the FFN column: the FFN stage of every layer of the table
+// on S.x_in, the last one's output in S.x_out (no attention, no position).
+template <bool kFull>
 __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     __shared__ Lds L;
-    const int wg = blockIdx.x, tid = threadIdx.x;
-    const int pos = *S.pos_dev;
-    const int token = *S.token;
-    if (pos < 0 || pos >= S.max_pos || token < 0 || token >= attn::kVocab) {
-        if (wg == 0 && tid == 0)
-            attn::raise(S.aws, (pos < 0 || pos >= S.max_pos) ? FLEET_MOE_ABORT_POSITION
-                                                             : FLEET_MOE_ABORT_TOKEN);
-        return;
+    const int wg = blockIdx.x, tid = fm_tid();
+    int pos = 0, token = 0;
+    if constexpr (kFull) {
+        pos = *S.pos_dev;
+        token = *S.token;
+        if (pos < 0 || pos >= S.max_pos || token < 0 || token >= attn::kVocab) {
+            if (wg == 0 && tid == 0)
+                attn::raise(S.aws, (pos < 0 || pos >= S.max_pos) ? FLEET_MOE_ABORT_POSITION
+                                                                 : FLEET_MOE_ABORT_TOKEN);
+            return;
+        }
     }
     // the call counts, written by the previous launch (plain loads: current
     // after the launch boundary)
-    const uint32_t ea = S.aws->epoch, em = S.mws->epoch, ed = S.dws->epoch, es = S.sws->epoch;
+    const uint32_t ea = kFull ? S.aws->epoch : 0u;
+    const uint32_t em = S.mws->epoch, ed = S.dws->epoch, es = S.sws->epoch;
     // exchange tags: 64 per step (2 per layer), so consecutive steps differ
     const uint32_t sbase = (es + 1u) * 64u;
     auto xtag = [&](int stage) { return ((sbase + (uint32_t)stage) & 0xffffu) << 16; };
-    uint32_t* xa = &S.sws->x[0][0][0];
-    uint32_t* xf = &S.sws->x[1][0][0];
+    uint32_t* xbuf[2] = {&S.sws->x[0][0][0], &S.sws->x[1][0][0]};
     int n_moe = 0, n_dense = 0;
 #if FLEET_STEP_TRACE
 #define STEP_TRACE(k) \
@@ -121,10 +129,14 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
 #define STEP_TRACE(k) do {} while (0)
 #endif
     STEP_TRACE(0);
+    // stage numbering: the decode step's attention of layer i is stage 2i + 1
+    // and its FFN 2i + 2; the column's FFN of layer i is stage i + 1. Stage s
+    // publishes into xbuf[s % 2] with tag xtag(s) and reads stage s - 1's.
     for (int i = 0; i < S.n_layers; ++i) {
         const fleet_step_layer& ly = S.layers[i];
         const bool last = i == S.n_layers - 1;
-        {
+        if constexpr (kFull) {
+            const int st = 2 * i + 1;
             attn::Params A{};
             A.norm_in = ly.attn.norm_in;
             A.qkv = ly.attn.qkv;
@@ -140,18 +152,20 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             A.eps = S.eps;
             A.ws = S.aws;
             A.epoch = ea + 1u + (uint32_t)i;
-            A.xin = i == 0 ? nullptr : xf;
+            A.xin = i == 0 ? nullptr : xbuf[(st - 1) % 2];
             A.xin_row = i == 0 ? S.embed + (int64_t)token * kHidden : nullptr;
-            A.xin_tag = xtag(2 * i);
-            A.xout = xa;
-            A.xout_tag = xtag(2 * i + 1);
+            A.xin_tag = xtag(st - 1);
+            A.xout = xbuf[st % 2];
+            A.xout_tag = xtag(st);
 #if FLEET_STEP_TRACE && FLEET_ATTN_TRACE
             A.trace = i == S.trace_layer ? S.trace_a : nullptr;
 #endif
             attn::attn_layer<true>(A, L.a);
+            __syncthreads();
+            STEP_TRACE(st);
         }
-        __syncthreads();
-        STEP_TRACE(1 + 2 * i);
+        const int st = kFull ? 2 * i + 2 : i + 1;
+        const bool first = !kFull && i == 0;
         if (ly.dense) {
             dense::Params D{};
             D.norm = ly.moe.norm;
@@ -160,10 +174,11 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             D.ws = S.dws;
             D.eps = S.eps;
             D.epoch = ed + 1u + (uint32_t)n_dense++;
-            D.xin = xa;
-            D.xin_tag = xtag(2 * i + 1);
-            D.xout = xf;
-            D.xout_tag = xtag(2 * i + 2);
+            D.xin = first ? nullptr : xbuf[(st - 1) % 2];
+            D.xin_f32 = first ? S.x_in : nullptr;
+            D.xin_tag = xtag(st - 1);
+            D.xout = xbuf[st % 2];
+            D.xout_tag = xtag(st);
             dense::dense_layer<true>(D, L.d);
         } else {
             decode::Params M{};
@@ -177,36 +192,40 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             M.eps = S.eps;
             M.scaling = S.scaling;
             M.epoch = em + 1u + (uint32_t)n_moe++;
-            M.xin = xa;
-            M.xin_tag = xtag(2 * i + 1);
-            M.xout = xf;
-            M.xout_tag = xtag(2 * i + 2);
+            M.xin = first ? nullptr : xbuf[(st - 1) % 2];
+            M.xin_f32 = first ? S.x_in : nullptr;
+            M.xin_tag = xtag(st - 1);
+            M.xout = xbuf[st % 2];
+            M.xout_tag = xtag(st);
 #if FLEET_STEP_TRACE && FLEET_MOE_TRACE
             M.trace = i == S.trace_layer ? S.trace_m : nullptr;
 #endif
             decode::moe_layer<true>(M, L.m);
         }
         __syncthreads();
-        STEP_TRACE(2 + 2 * i);
+        STEP_TRACE(st);
     }
-    {
+    if constexpr (kFull) {
         attn::HeadParams H{};
         H.norm = S.final_norm;
         H.W = S.lm_head;
         H.eps = S.eps;
         H.logits = S.logits;
         H.ws = S.aws;
-        H.xin = xf;
+        H.xin = xbuf[(2 * S.n_layers) % 2];
         H.xin_tag = xtag(2 * S.n_layers);
         H.epoch = es + 1u;
         H.token_out = S.token_out;
         H.token_next = S.token_next;
         H.pos_advance = S.pos_dev;
         attn::lmhead_body<true>(H, L.h);
+        STEP_TRACE(2 * S.n_layers + 1);
     }
-    STEP_TRACE(2 * S.n_layers + 1);
+    // workgroup 0 advances the call counts: the argmax (decode step) or the
+    // last FFN stage's h exchange (column) needed every workgroup, so every
+    // workgroup has read them
     if (wg == 0 && tid == 0) {
-        st_agent(&S.aws->epoch, ea + (uint32_t)S.n_layers);
+        if constexpr (kFull) st_agent(&S.aws->epoch, ea + (uint32_t)S.n_layers);
         st_agent(&S.mws->epoch, em + (uint32_t)n_moe);
         st_agent(&S.dws->epoch, ed + (uint32_t)n_dense);
         st_agent(&S.sws->epoch, es + 1u);
@@ -259,7 +278,7 @@ extern "C" int fleet_decode_step(const fleet_step_model* model, const int32_t* t
         !aligned(workspace, 256))
         return FLEET_MOE_ERR_ARG;
     if (workspace_bytes < step::kBytes) return FLEET_MOE_ERR_WORKSPACE;
-    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&step::step_kernel),
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&step::step_kernel<true>),
                                          step::kThreads, step::kWG))
         return e;
     uint8_t* w = static_cast<uint8_t*>(workspace);
@@ -294,7 +313,44 @@ extern "C" int fleet_decode_step(const fleet_step_model* model, const int32_t* t
     S.trace_m = g_step_trace_m;
     S.trace_layer = g_step_trace_layer;
 #endif
-    hipLaunchKernelGGL(step::step_kernel, dim3(step::kWG), dim3(step::kThreads), 0, stream, S);
+    hipLaunchKernelGGL(step::step_kernel<true>, dim3(step::kWG), dim3(step::kThreads), 0, stream,
+                       S);
+    return (int)hipGetLastError();
+}
+
+extern "C" int fleet_ffn_column(const fleet_step_layer* layers, int32_t n_layers, const float* x,
+                                float* x_out, void* workspace, size_t workspace_bytes,
+                                const fleet_moe_dims* dims, hipStream_t stream) {
+    if (!dims) return FLEET_MOE_ERR_ARG;
+    if (int e = fleet_moe_check_dims(dims)) return e;
+    if (!layers || n_layers < 1 || n_layers > step::kMaxLayers || !x || !x_out || !workspace)
+        return FLEET_MOE_ERR_ARG;
+    if (!aligned(layers, 8) || !aligned(x, 16) || !aligned(x_out, 4) || !aligned(workspace, 256))
+        return FLEET_MOE_ERR_ARG;
+    if (workspace_bytes < step::kBytes) return FLEET_MOE_ERR_WORKSPACE;
+    if (int e = fleet_moe_check_resident(reinterpret_cast<const void*>(&step::step_kernel<false>),
+                                         step::kThreads, step::kWG))
+        return e;
+    uint8_t* w = static_cast<uint8_t*>(workspace);
+    step::Params S{};
+    S.layers = layers;
+    S.n_layers = n_layers;
+    S.x_in = x;
+    S.x_out = x_out;
+    S.eps = dims->rms_eps;
+    S.scaling = dims->routed_scaling;
+    S.aws = reinterpret_cast<attn::Workspace*>(w + step::kOffAttn);
+    S.mws = reinterpret_cast<decode::Workspace*>(w + step::kOffMoe);
+    S.dws = reinterpret_cast<dense::Workspace*>(w + step::kOffDense);
+    S.sws = reinterpret_cast<step::Workspace*>(w + step::kOffStep);
+#if FLEET_STEP_TRACE
+    S.trace = g_step_trace;
+    S.trace_a = g_step_trace_a;
+    S.trace_m = g_step_trace_m;
+    S.trace_layer = g_step_trace_layer;
+#endif
+    hipLaunchKernelGGL(step::step_kernel<false>, dim3(step::kWG), dim3(step::kThreads), 0, stream,
+                       S);
     return (int)hipGetLastError();
 }
 

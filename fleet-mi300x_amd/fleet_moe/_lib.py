@@ -94,6 +94,9 @@ SYMBOLS = [
      [POINTER(FleetStepModel), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
       c_void_p, c_size_t, POINTER(FleetMoeDims), c_void_p]),
     ("fleet_decode_step_status", c_int, [c_void_p, POINTER(ctypes.c_uint32), c_void_p]),
+    ("fleet_ffn_column", c_int,
+     [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, POINTER(FleetMoeDims),
+      c_void_p]),
     ("fleet_embed", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("fleet_lm_head_argmax", c_int,
      [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

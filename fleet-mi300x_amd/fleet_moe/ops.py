@@ -246,7 +246,8 @@ class FfnColumn:
     294-302 without the attention half). `blob` is the packed uint8 device
     tensor of `layout` (fleet_moe.layout.column_layout)."""
 
-    def __init__(self, blob: torch.Tensor, layout: Layout, dims: MoeDims = DSV2_LITE):
+    def __init__(self, blob: torch.Tensor, layout: Layout, dims: MoeDims = DSV2_LITE,
+                 fused: bool = True):
         self.blob, self.layout, self.dims = blob, layout, dims
         self.n_layers = int(layout.scalars["layers"])
         self.first_k_dense = int(layout.scalars["first_k_dense"])
@@ -254,6 +255,21 @@ class FfnColumn:
                     for i in range(self.first_k_dense, self.n_layers)}
         self.decoder = LayerDecoder(dims, device=blob.device)
         self.dense = DenseDecoder(dims, int(layout.scalars["dense_inter"]), device=blob.device)
+        self.fused = bool(fused)
+        if self.fused:
+            lib = _lib.load()
+            rows = (_lib.FleetStepLayer * self.n_layers)()
+            for i in range(self.n_layers):
+                if i < self.first_k_dense:
+                    rows[i].moe = _lib.FleetMoeLayer(self._addr(f"L{i}.norm_post"), None, None, 0,
+                                                     None)
+                    rows[i].dense = self._addr(f"L{i}.dense")
+                else:
+                    rows[i].moe = self.moe[i].c_layer()
+            raw = bytes(memoryview(rows).cast("B"))
+            self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(blob.device)
+            n = lib.fleet_decode_step_workspace_bytes(ctypes.byref(self.decoder._dims))
+            self.step_ws = torch.zeros(n, dtype=torch.uint8, device=blob.device)
 
     def _addr(self, name: str) -> int:
         return self.blob.data_ptr() + self.layout.tensors[name].offset
@@ -266,12 +282,25 @@ class FfnColumn:
             self.decoder.decode_into(self.moe[i], x, x_out, stream=stream)
 
     def run_into(self, x: torch.Tensor, stream=None) -> None:
-        """All layers in place on x (fp32[hidden] on the device); no allocation."""
+        """All layers in place on x (fp32[hidden] on the device); no allocation.
+        fused: one launch (fleet_ffn_column); else one launch per layer."""
+        if self.fused:
+            rc = _lib.load().fleet_ffn_column(
+                self.table.data_ptr(), self.n_layers, _ptr(x), _ptr(x), _ptr(self.step_ws),
+                self.step_ws.numel(), ctypes.byref(self.decoder._dims), _stream(stream))
+            _lib.check(rc, "fleet_ffn_column")
+            return
         for i in range(self.n_layers):
             self.layer_into(i, x, x, stream)
 
     def status(self) -> int:
-        return self.decoder.status() | self.dense.status()
+        st = self.decoder.status() | self.dense.status()
+        if self.fused:
+            v = ctypes.c_uint32(0)
+            _lib.check(_lib.load().fleet_decode_step_status(_ptr(self.step_ws), ctypes.byref(v),
+                                                            None), "fleet_decode_step_status")
+            st |= int(v.value)
+        return st
 
 
 class AttnDecoder:
@@ -348,7 +377,7 @@ class Decoder:
         self.sin = torch.from_numpy(sin).to(dev)
         self.cache = torch.zeros((self.n_layers, self.max_pos, 576), dtype=torch.int16,
                                  device=dev)
-        self.ffn = FfnColumn(blob, layout, dims)
+        self.ffn = FfnColumn(blob, layout, dims, fused=False)
         self.attn = AttnDecoder(dims, device=dev)
         self.attn_layers = [self._attn_layer(i) for i in range(self.n_layers)]
         self.x = torch.zeros(dims.hidden, dtype=torch.float32, device=dev)

@@ -287,6 +287,17 @@ int fleet_decode_step(const fleet_step_model* model, const int32_t* token, int32
  * OR over its stages), read synchronously on `stream`. */
 int fleet_decode_step_status(const void* workspace, uint32_t* status, hipStream_t stream);
 
+/* The FFN half of every layer of the table chained on x in ONE launch (the
+ * benchmark's config 3, reference_decode.py:294-302 without the attention
+ * half): x_out = ffn_{n-1}(... ffn_0(x)), each x' = bf16(x + ffn(rms_norm(x)))
+ * with the layer's dense or MoE FFN; equal bit for bit to chaining
+ * fleet_moe_dense_decode / fleet_moe_layer_decode. layers: DEVICE array
+ * (only the FFN fields are read); x, x_out: fp32[hidden] (may be equal);
+ * workspace: as fleet_decode_step's (status: fleet_decode_step_status). */
+int fleet_ffn_column(const fleet_step_layer* layers, int32_t n_layers, const float* x,
+                     float* x_out, void* workspace, size_t workspace_bytes,
+                     const fleet_moe_dims* dims, hipStream_t stream);
+
 /* x = embed[*token] as fp32 (the EMBED task, src/kernels/fleet_kernel.hip:
  * 68-78). token: a device int32, so a decode loop can feed the previous
  * step's argmax without a host round trip; a token outside [0, 102400) sets

@@ -101,11 +101,15 @@ def test_column_four_layers_teacher_forced():
     col = build(4, seed=3)
     x0 = orc.bf16_round(synth.hidden_inputs(40, 1)[0])
     out = run_and_check(col, x0, layers={0, 1, 2, 3})
-    # run_into (in place, no allocation) gives the same stream, bit for bit
-    x = torch.from_numpy(x0).cuda()
-    col.run_into(x)
-    torch.cuda.synchronize()
-    np.testing.assert_array_equal(x.cpu().numpy(), out)
+    # run_into (in place, no allocation, one launch: fleet_ffn_column) gives
+    # the same stream, bit for bit, on every call
+    assert col.fused
+    for _ in range(3):
+        x = torch.from_numpy(x0).cuda()
+        col.run_into(x)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(x.cpu().numpy(), out)
+    assert col.status() == 0
     del col
     torch.cuda.empty_cache()
 
@@ -117,5 +121,11 @@ def test_column_full_27_layers():
     x0 = orc.bf16_round(synth.hidden_inputs(41, 1)[0])
     out = run_and_check(col, x0, layers={0, 1, 26})
     assert np.all(np.isfinite(out))
+    # the 27 layers in one launch (fleet_ffn_column): the same output bit for bit
+    x = torch.from_numpy(x0).cuda()
+    col.run_into(x)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(x.cpu().numpy(), out)
+    assert col.status() == 0
     del col
     torch.cuda.empty_cache()
