@@ -506,25 +506,17 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
     const int wg = blockIdx.x, tid = fm_tid(), lane = tid & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: branches on it are scalar
     Workspace* ws = P.ws;
-    const int pos = kMega ? P.pos_host : (P.pos_dev ? *P.pos_dev : P.pos_host);
-    if (!kMega && (pos < 0 || pos >= P.max_pos)) {
-        if (wg == 0 && tid == 0) raise(ws, FLEET_MOE_ABORT_POSITION);
-        return;
+    // the position: the step's, the host's, or *pos_dev through the scalar
+    // cache (invalidated at every launch, so current after the launch
+    // boundary), its latency hidden behind the position-independent loads
+    // below; a bad position is rejected only after they are issued
+    int pos = P.pos_host;
+    if constexpr (!kMega) {
+        if (P.pos_dev) pos = *(const __attribute__((address_space(4))) int32_t*)P.pos_dev;
     }
     ATTN_TRACE(0);
     const int h = (wg & 7) + 8 * ((wg >> 3) & 1);
     const int k = wg >> 4;
-    const int n_pos = pos + 1;
-    const int C = (n_pos + kChunks - 1) / kChunks;      // positions per chunk
-    const int n_used = (n_pos + C - 1) / C;             // chunks holding positions
-    // S3's (head, chunk): XCD x (wg % 8) takes chunks 2x and 2x + 1 of all 16 heads, so
-    // each cached row is fetched into one XCD's L2 only
-    const int h3 = (wg >> 3) & 15;
-    const int k3 = 2 * (wg & 7) + (wg >> 7);
-    const int t0 = k3 * C;
-    const int t1 = min(t0 + C, n_pos);
-    const bool has_rows = k3 < n_used;
-    const bool last = k3 == n_used - 1;                 // the chunk holding `pos`
 
     // ---- the inputs of the first stage
     // the call count, written by the previous launch: a plain load (after the
@@ -534,15 +526,13 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
     const uint32_t tag = (epoch & 0xffffu) << 16;
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (!kMega) xv = reinterpret_cast<const float4*>(P.x)[tid];
-    const uint2 gb = P.norm_in ? reinterpret_cast<const uint2*>(P.norm_in)[tid]
+    const uint2 gb = P.norm_in ? ld_global_u2(P.norm_in, tid)
                                : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
     float x_own = (!kMega && tid < kOpRows) ? P.x[kOpRows * wg + tid] : 0.f;
-    // S3's per-position inputs, needed after several hand-offs: this
-    // position's RoPE angle (thread i < 64: element i) and the kv_a_layernorm
-    // weight (thread i: element i)
-    const float cs_t = tid < kRope ? P.cos[(int64_t)pos * kRope + tid] : 0.f;
-    const float sn_t = tid < kRope ? P.sin[(int64_t)pos * kRope + tid] : 0.f;
-    const float kvn_t = P.kv_a_norm ? __uint_as_float((uint32_t)P.kv_a_norm[tid] << 16) : 1.0f;
+    // the kv_a_layernorm weight (thread i: element i), needed in S3; raw bf16
+    // bits, widened where used (widened here, the wave would wait for this
+    // load before issuing the weight rows below)
+    const uint32_t kvn_b = P.kv_a_norm ? (uint32_t)ld_global(P.kv_a_norm + tid) : 0x3f80u;
     // q rows of head h: 12 per workgroup (i = wave, and wave + 8 for waves
     // 0..3); kv_a rows: 3072 + wg + 256 i for waves 4..6 (i = wave - 4, the
     // last only for wg < 64)
@@ -557,6 +547,24 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) wq1[m] = u32x4{0u, 0u, 0u, 0u};
     }
+    if (!kMega && (pos < 0 || pos >= P.max_pos)) {
+        if (wg == 0 && tid == 0) raise(ws, FLEET_MOE_ABORT_POSITION);
+        return;
+    }
+    const int n_pos = pos + 1;
+    const int C = (n_pos + kChunks - 1) / kChunks;      // positions per chunk
+    const int n_used = (n_pos + C - 1) / C;             // chunks holding positions
+    // S3's (head, chunk): XCD x (wg % 8) takes chunks 2x and 2x + 1 of all 16 heads, so
+    // each cached row is fetched into one XCD's L2 only
+    const int h3 = (wg >> 3) & 15;
+    const int k3 = 2 * (wg & 7) + (wg >> 7);
+    const int t0 = k3 * C;
+    const int t1 = min(t0 + C, n_pos);
+    const bool has_rows = k3 < n_used;
+    const bool last = k3 == n_used - 1;                 // the chunk holding `pos`
+    // this position's RoPE angle (thread i < 64: element i), needed in S3
+    const float cs_t = tid < kRope ? P.cos[(int64_t)pos * kRope + tid] : 0.f;
+    const float sn_t = tid < kRope ? P.sin[(int64_t)pos * kRope + tid] : 0.f;
     if constexpr (kMega) {
         // x: the embedding row, or every workgroup's published rows
         if (P.xin_row) {
@@ -598,20 +606,24 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
         P.kv_b + ((int64_t)h * kKvbRowsPerHead + kUkRows * wave + (lane >> 2)) * kLora +
         kQcCols * k + 8 * (lane & 3)));
     // this wave's first cache rows of the chunk (rows before `pos`; row `pos`
-    // is derived from kv_a below)
+    // is derived from kv_a below), one row at a time: the wave waits for each
+    // row before issuing the next. Issued all at once, these rows (20 MB of
+    // L2 reads over the chip) compete with the first stage's weight rows of
+    // the workgroups still streaming them, and the layer takes ~2 us longer.
     u32x4 c8[kBatch];
-    float kp[kBatch];
+    uint32_t kp[kBatch];
     const int t_end = min(t1, pos);
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
         const int t = t0 + wave + kWaves * i;
         if (t < t_end) {
             const uint16_t* row = P.cache + (int64_t)t * kRowElems;
-            c8[i] = reinterpret_cast<const u32x4*>(row)[lane];
-            kp[i] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
+            c8[i] = ld_global(reinterpret_cast<const u32x4*>(row) + lane);
+            kp[i] = ld_global(row + kLora + lane);
+            asm volatile("" : "+v"(kp[i]));                // the wait
         } else {
             c8[i] = u32x4{0u, 0u, 0u, 0u};
-            kp[i] = 0.f;
+            kp[i] = 0u;
         }
     }
 
@@ -725,7 +737,9 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
             for (int w = 0; w < kWaves; ++w) ssq += L.red[w];
             const float var = (float)(ssq / (double)kLora);
             const float inv = __fdiv_rn(1.0f, sqrt_rn(var + P.eps));
-            const float g = kvn_t;
+            uint32_t gbits = kvn_b;
+            asm volatile("" : "+v"(gbits));                // keeps the widening here
+            const float g = __uint_as_float(gbits << 16);
             const uint16_t cb = (uint16_t)bf16_bits(bf16r(bf16r(c * inv) * g));
             L.u.s3.row[tid] = cb;
             uint16_t kb = 0;
@@ -735,8 +749,8 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
             }
             if (h3 == 0) {
                 uint16_t* crow = P.cache + (int64_t)pos * kRowElems;
-                crow[tid] = cb;
-                if (tid < kRope) crow[kLora + tid] = kb;
+                st_global(crow + tid, cb);
+                if (tid < kRope) st_global(crow + kLora + tid, kb);
             }
         }
         __syncthreads();
@@ -762,14 +776,14 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
                 for (int i = 0; i < kBatch; ++i) {
                     const int t = min(base + kWaves * i, t_end - 1);   // clamped: a real row
                     const uint16_t* row = P.cache + (int64_t)t * kRowElems;
-                    c8[i] = reinterpret_cast<const u32x4*>(row)[lane];
-                    kp[i] = __uint_as_float((uint32_t)row[kLora + lane] << 16);
+                    c8[i] = ld_global(reinterpret_cast<const u32x4*>(row) + lane);
+                    kp[i] = ld_global(row + kLora + lane);
                 }
             }
             double a[kSum];
 #pragma unroll
             for (int i = 0; i < kSum; ++i)
-                a[i] = i < kBatch ? dot8_xd(c8[i], qd, (double)(kp[i] * qp)) : 0.0;
+                a[i] = i < kBatch ? dot8_xd(c8[i], qd, (double)(__uint_as_float(kp[i] << 16) * qp)) : 0.0;
             const double tot = wave_msum64(a);
             const bool valid = ri < kBatch && base + kWaves * ri < t_end;
             const double sv = valid ? tot * P.scale : -INFINITY;
@@ -993,7 +1007,7 @@ __device__ __forceinline__ void lmhead_body(const HeadParams& H, HeadLds& S) {
     float* logits = H.logits;
     Workspace* ws = H.ws;
     const int wave = fm_tid() >> 6, lane = fm_tid() & (kLanes - 1);
-    const uint2 gb = H.norm ? reinterpret_cast<const uint2*>(H.norm)[fm_tid()]
+    const uint2 gb = H.norm ? ld_global_u2(H.norm, fm_tid())
                             : make_uint2(0x3f803f80u, 0x3f803f80u);
     float4 xv;
     if constexpr (kMega)

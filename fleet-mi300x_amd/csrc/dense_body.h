@@ -107,7 +107,7 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L) {
     const uint32_t tag = (epoch & 0xffffu) << 16;
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (!kMega) xv = reinterpret_cast<const float4*>(P.x)[tid];
-    const uint2 gb = P.norm ? reinterpret_cast<const uint2*>(P.norm)[tid]
+    const uint2 gb = P.norm ? ld_global_u2(P.norm, tid)
                             : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
     const u32x4* gu = reinterpret_cast<const u32x4*>(P.w);
     const int n_items = pairs_of(wg);

@@ -466,7 +466,7 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
     const uint32_t tag = (epoch & 0xffffu) << 16;
     float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (!kMega) xv = reinterpret_cast<const float4*>(P.x)[tid];
-    const uint2 gb = P.norm ? reinterpret_cast<const uint2*>(P.norm)[tid]
+    const uint2 gb = P.norm ? ld_global_u2(P.norm, tid)
                             : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
     const int rrow0 = wave * kRouterRowsPerWave;
     u32x4 ra[4][4];
@@ -474,12 +474,12 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            ra[r][m] = P.router[(int64_t)(rrow0 + r) * kRowChunks + lane + kLanes * m];
+            ra[r][m] = ld_global(P.router + (int64_t)(rrow0 + r) * kRowChunks + lane + kLanes * m);
     const bool exact_row = ctl && wg < kRouted;
     u32x4 er[4];
     if (exact_row) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) er[m] = P.router[(int64_t)wg * kRowChunks + lane + kLanes * m];
+        for (int m = 0; m < 4; ++m) er[m] = ld_global(P.router + (int64_t)wg * kRowChunks + lane + kLanes * m);
     }
     u32x4 bufA[8];
     int cur;
@@ -534,7 +534,7 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            rb[r][m] = P.router[(int64_t)(rrow0 + 4 + r) * kRowChunks + lane + kLanes * m];
+            rb[r][m] = ld_global(P.router + (int64_t)(rrow0 + 4 + r) * kRowChunks + lane + kLanes * m);
     __syncthreads();
     u32x4 xq[4];
 #pragma unroll

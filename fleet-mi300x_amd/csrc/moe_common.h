@@ -27,6 +27,29 @@ __device__ __forceinline__ int fm_tid() {
     return t;
 }
 
+// Loads through global-memory pointers. A pointer read from memory (the
+// whole-step kernel's layer table) rather than taken from a kernel argument
+// has no known address space, and the compiler would emit flat loads for it,
+// which also count against the LDS wait counter: every LDS wait would then
+// wait for the weight stream too. Loading through an address_space(1)
+// pointer emits global loads whatever the pointer's origin.
+template <class T>
+using gmem_ptr = const __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ T ld_global(const T* p) {
+    return *(gmem_ptr<T>)p;
+}
+// (uint2 through a 64-bit load: the vector type's copy constructor takes a
+// generic reference and would turn the load back into a flat one)
+__device__ __forceinline__ uint2 ld_global_u2(const void* p, int i) {
+    const uint64_t v = ld_global(reinterpret_cast<const uint64_t*>(p) + i);
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+template <class T>
+__device__ __forceinline__ void st_global(T* p, T v) {
+    *(__attribute__((address_space(1))) T*)p = v;
+}
+
 // DeepSeek-V2-Lite MoE shape (reference/dsv2lite_config.json).
 constexpr int kHidden = 2048;
 constexpr int kInter = 1408;          // routed expert intermediate
@@ -48,7 +71,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // exactly once per call, so they should not displace the small shared
 // vectors from L2).
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
-    return __builtin_nontemporal_load(p);
+    return __builtin_nontemporal_load((gmem_ptr<u32x4>)p);
 }
 
 __device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
