@@ -98,14 +98,39 @@ union Lds {
 // kFull: the decode step (embed, attention and FFN of every layer, lm_head,
 // argmax). Otherwise the FFN column: the FFN stage of every layer of the table
 // on S.x_in, the last one's output in S.x_out (no attention, no position).
+// A word written by an earlier launch, read through the scalar cache (which
+// every launch starts with invalidated): a uniform value in SGPRs, its wait
+// independent of the vector loads in flight.
+template <class T>
+__device__ __forceinline__ T ld_launch_const(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
+
+constexpr int kLayerWords = sizeof(fleet_step_layer) / 8;
+static_assert(sizeof(fleet_step_layer) % 8 == 0, "the layer table is copied in 8-byte words");
+static_assert(kMaxLayers * kLayerWords <= 2 * kThreads, "two table words per thread at most");
+
 template <bool kFull>
 __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     __shared__ Lds L;
+    // The layer table, copied into LDS once per launch: read from global
+    // memory at each stage, a stage's weight pointers would arrive about a
+    // microsecond after the stage starts, and every weight load waits for them.
+    __shared__ uint64_t tbl_words[kMaxLayers * kLayerWords];
     const int wg = blockIdx.x, tid = fm_tid();
+    {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(S.layers);
+        const int n = S.n_layers * kLayerWords;
+        const uint64_t a = tid < n ? ld_global(src + tid) : 0ull;
+        const uint64_t b = tid + kThreads < n ? ld_global(src + tid + kThreads) : 0ull;
+        if (tid < n) tbl_words[tid] = a;
+        if (tid + kThreads < n) tbl_words[tid + kThreads] = b;
+    }
+    const fleet_step_layer* tbl = reinterpret_cast<const fleet_step_layer*>(tbl_words);
     int pos = 0, token = 0;
     if constexpr (kFull) {
-        pos = *S.pos_dev;
-        token = *S.token;
+        pos = ld_launch_const(S.pos_dev);
+        token = ld_launch_const(S.token);
         if (pos < 0 || pos >= S.max_pos || token < 0 || token >= attn::kVocab) {
             if (wg == 0 && tid == 0)
                 attn::raise(S.aws, (pos < 0 || pos >= S.max_pos) ? FLEET_MOE_ABORT_POSITION
@@ -115,8 +140,9 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     }
     // the call counts, written by the previous launch (plain loads: current
     // after the launch boundary)
-    const uint32_t ea = kFull ? S.aws->epoch : 0u;
-    const uint32_t em = S.mws->epoch, ed = S.dws->epoch, es = S.sws->epoch;
+    const uint32_t ea = kFull ? ld_launch_const(&S.aws->epoch) : 0u;
+    const uint32_t em = ld_launch_const(&S.mws->epoch), ed = ld_launch_const(&S.dws->epoch),
+                   es = ld_launch_const(&S.sws->epoch);
     // exchange tags: 64 per step (2 per layer), so consecutive steps differ
     const uint32_t sbase = (es + 1u) * 64u;
     auto xtag = [&](int stage) { return ((sbase + (uint32_t)stage) & 0xffffu) << 16; };
@@ -128,12 +154,13 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
 #else
 #define STEP_TRACE(k) do {} while (0)
 #endif
+    __syncthreads();                          // the table
     STEP_TRACE(0);
     // stage numbering: the decode step's attention of layer i is stage 2i + 1
     // and its FFN 2i + 2; the column's FFN of layer i is stage i + 1. Stage s
     // publishes into xbuf[s % 2] with tag xtag(s) and reads stage s - 1's.
     for (int i = 0; i < S.n_layers; ++i) {
-        const fleet_step_layer& ly = S.layers[i];
+        const fleet_step_layer& ly = tbl[i];
         const bool last = i == S.n_layers - 1;
         if constexpr (kFull) {
             const int st = 2 * i + 1;
