@@ -496,13 +496,52 @@ struct Lds {
     } u;
 };
 
+// The first stage's rows of this wave: q rows of head h, 12 per workgroup
+// (i = wave, and wave + 8 for waves 0..3); kv_a rows 3072 + wg + 256 i for
+// waves 4..6 (i = wave - 4, the last only for wg < 64). w[0..3] holds row r0,
+// w[4..7] row r1 (zeros where the wave has no second row).
+__device__ __forceinline__ void first_rows(const uint16_t* qkv, int& r0, int& r1,
+                                           u32x4 (&w)[8], bool issue) {
+    const int wg = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(fm_tid() >> 6);
+    const int lane = fm_tid() & (kLanes - 1);
+    const int h = (wg & 7) + 8 * ((wg >> 3) & 1);
+    const int k = wg >> 4;
+    r0 = h * (kNope + kRope) + k + kChunks * wave;
+    r1 = wave < 4 ? h * (kNope + kRope) + k + kChunks * (wave + kWaves)
+       : wave < 7 ? kQDim + wg + kWG * (wave - 4) : kQkvRows;
+    if (!issue) return;
+    const u32x4* a = reinterpret_cast<const u32x4*>(qkv + (int64_t)r0 * kHidden);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) w[m] = ld_stream(a + lane + kLanes * m);
+    if (r1 < kQkvRows) {
+        const u32x4* b = reinterpret_cast<const u32x4*>(qkv + (int64_t)r1 * kHidden);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) w[4 + m] = ld_stream(b + lane + kLanes * m);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) w[4 + m] = u32x4{0u, 0u, 0u, 0u};
+    }
+}
+// The whole-step kernel's hand-over: the stage before this one issues these
+// rows once its own last wait is done (into `pre`), so they are in flight
+// while that stage finishes and the residual is handed over.
+__device__ __forceinline__ void issue_first_rows(const uint16_t* qkv, u32x4 (&pre)[8]) {
+    int r0, r1;
+    first_rows(qkv, r0, r1, pre, true);
+}
+
 // The layer. kMega: inside the whole-step kernel (fleet_decode_step): the
 // call count and the position come from the step (P.epoch, P.pos_host), x
 // from the tagged exchange buffer P.xin (or, for layer 0, the bf16 embedding
 // row P.xin_row), and x_out goes to the exchange buffer P.xout (and to
-// P.x_out when that is not null).
-template <bool kMega>
-__device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
+// P.x_out when that is not null). `pre` holds the first stage's rows; with
+// pre_in they were issued by the stage before (otherwise here). `next` runs
+// once this layer's last wait is done: the whole-step kernel issues the next
+// stage's first loads there.
+template <bool kMega, class Next>
+__device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)[8], bool pre_in,
+                                           Next&& next) {
     const int wg = blockIdx.x, tid = fm_tid(), lane = tid & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: branches on it are scalar
     Workspace* ws = P.ws;
@@ -533,20 +572,10 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
     // bits, widened where used (widened here, the wave would wait for this
     // load before issuing the weight rows below)
     const uint32_t kvn_b = P.kv_a_norm ? (uint32_t)ld_global(P.kv_a_norm + tid) : 0x3f80u;
-    // q rows of head h: 12 per workgroup (i = wave, and wave + 8 for waves
-    // 0..3); kv_a rows: 3072 + wg + 256 i for waves 4..6 (i = wave - 4, the
-    // last only for wg < 64)
-    const int r0 = h * (kNope + kRope) + k + kChunks * wave;
-    const int r1 = wave < 4 ? h * (kNope + kRope) + k + kChunks * (wave + kWaves)
-                 : wave < 7 ? kQDim + wg + kWG * (wave - 4) : kQkvRows;
-    u32x4 wq0[4], wq1[4];
-    load_row(P.qkv, r0, wq0);
-    if (r1 < kQkvRows) {
-        load_row(P.qkv, r1, wq1);
-    } else {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) wq1[m] = u32x4{0u, 0u, 0u, 0u};
-    }
+    int r0, r1;
+    first_rows(P.qkv, r0, r1, pre, !(kMega && pre_in));
+    const u32x4 wq0[4] = {pre[0], pre[1], pre[2], pre[3]};
+    const u32x4 wq1[4] = {pre[4], pre[5], pre[6], pre[7]};
     if (!kMega && (pos < 0 || pos >= P.max_pos)) {
         if (wg == 0 && tid == 0) raise(ws, FLEET_MOE_ABORT_POSITION);
         return;
@@ -930,6 +959,7 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L) {
         u32x4 v;
         poll16(ws->out_t[wg % kOutCopies], 4 * (256 * wave + 4 * lane), true, tag, v, ws);
         ATTN_TRACE(14);
+        next();
         reinterpret_cast<uint2*>(L.u.s5.outv)[64 * wave + lane] =
             make_uint2((v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16));
         __syncthreads();

@@ -7,7 +7,8 @@ namespace attn {
 
 __global__ __launch_bounds__(kThreads, 1) void attn_layer_kernel(Params P) {
     __shared__ Lds L;
-    attn_layer<false>(P, L);
+    u32x4 pre[8];
+    attn_layer<false>(P, L, pre, false, [] {});
 }
 
 __global__ __launch_bounds__(kThreads, 1) void embed_kernel(const uint16_t* E, const int32_t* token,

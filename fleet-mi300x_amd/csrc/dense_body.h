@@ -95,8 +95,27 @@ __device__ __forceinline__ void issue_pair(const u32x4* base, int lane, u32x4 (&
 // call count comes from the step (P.epoch), x from the tagged exchange buffer
 // P.xin and x_out goes to the exchange buffer P.xout (and to P.x_out when
 // that is not null).
-template <bool kMega>
-__device__ __forceinline__ void dense_layer(const Params& P, Lds& L) {
+// A wave's first gate/up pair (pair wg + 256 wave, if the workgroup has
+// that many; zeros otherwise), issued into `b`. The whole-step kernel issues
+// it from the stage before this one, once that stage's last wait is done.
+__device__ __forceinline__ void issue_first_pair(const uint16_t* w, u32x4 (&b)[8]) {
+    const int wg = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(fm_tid() >> 6);
+    if (wave < pairs_of(wg)) {
+        issue_pair(reinterpret_cast<const u32x4*>(w) + (int64_t)(wg + kWG * wave) * 2 * kRowChunks,
+                   fm_tid() & (kLanes - 1), b);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) b[m] = u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+// `pre` is the first pair's buffer; with pre_in the pair was issued by the
+// stage before (otherwise here). `next` runs once this layer's last wait is
+// done: the whole-step kernel issues the next stage's first loads there.
+template <bool kMega, class Next>
+__device__ __forceinline__ void dense_layer(const Params& P, Lds& L, u32x4 (&pre)[8], bool pre_in,
+                                            Next&& next) {
     const int wg = blockIdx.x, tid = fm_tid();
     const int wave = tid >> 6, lane = tid & (kLanes - 1);
     Workspace* ws = P.ws;
@@ -111,9 +130,9 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L) {
                             : make_uint2(0x3f803f80u, 0x3f803f80u);   // bf16 1.0
     const u32x4* gu = reinterpret_cast<const u32x4*>(P.w);
     const int n_items = pairs_of(wg);
-    u32x4 buf[8];
+    u32x4 (&buf)[8] = pre;
     int cur = wave < n_items ? wave : -1;
-    if (cur >= 0) issue_pair(gu + (int64_t)(wg + kWG * cur) * 2 * kRowChunks, lane, buf);
+    if (!(kMega && pre_in)) issue_first_pair(P.w, buf);
     if (tid == 0) L.next = kWaves;
     if constexpr (kMega) {
         // x: every workgroup's published rows (polled behind this wave's first
@@ -277,6 +296,7 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L) {
         for (int i = 0; i < kDnIters; ++i) acc = dot8_x(W[i], h_chunk(i), acc);
         out = bf16r((float)wave_sum64(acc));
     }
+    next();
     if (lane == 0) {
         const float xo = bf16r((kMega ? L.xraw[n] : P.x[n]) + out);
         if (!kMega || P.x_out) P.x_out[n] = xo;

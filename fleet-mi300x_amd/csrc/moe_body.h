@@ -441,12 +441,34 @@ __device__ __forceinline__ bool wait_routing(Lds& L) {
     return st == 2;
 }
 
+// A streaming wave's first pair (shared pair wg + 256 wave; the control wave
+// has none), issued into `b`. The whole-step kernel issues it from the stage
+// before this one, once that stage's last wait is done, so it is in flight
+// while that stage finishes and the residual is handed over.
+__device__ __forceinline__ void issue_first_pair(const uint16_t* shared, u32x4 (&b)[8]) {
+    const int wave = __builtin_amdgcn_readfirstlane(fm_tid() >> 6);
+    if (wave == kCtlWave) {
+        // written all the same: a buffer that is not rewritten on every path
+        // would stay live through the stages in between
+#pragma unroll
+        for (int m = 0; m < 8; ++m) b[m] = u32x4{0u, 0u, 0u, 0u};
+        return;
+    }
+    issue_pair(reinterpret_cast<const u32x4*>(shared) +
+                   (int64_t)(blockIdx.x + kWG * wave) * 2 * kRowChunks,
+               fm_tid() & (kLanes - 1), b);
+}
+
 // The layer. kMega: inside the whole-step kernel (fleet_decode_step): the
 // call count comes from the step (P.epoch), x from the tagged exchange buffer
 // P.xin and x_out goes to the exchange buffer P.xout (and to P.x_out when
-// that is not null).
-template <bool kMega>
-__device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
+// that is not null). `pre` is the first pair's buffer; with pre_in the pair
+// was issued by the stage before (otherwise here). `next` runs once this
+// layer's last wait is done: the whole-step kernel issues the next stage's
+// first loads there.
+template <bool kMega, class Next>
+__device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[8], bool pre_in,
+                                          Next&& next) {
     const int wg = blockIdx.x;
     const int tid = fm_tid();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: branches on it are scalar
@@ -481,15 +503,18 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) er[m] = ld_global(P.router + (int64_t)wg * kRowChunks + lane + kLanes * m);
     }
-    u32x4 bufA[8];
+    u32x4 (&bufA)[8] = pre;
     int cur;
-    if (!ctl)
-        issue_pair(reinterpret_cast<const u32x4*>(P.shared) +
-                       (int64_t)(wg + kWG * wave) * 2 * kRowChunks,
-                   lane, bufA);
+    if (!(kMega && pre_in)) issue_first_pair(P.shared, bufA);
     FLEET_TRACE(0);
-    if (tid == 0) { L.next = kWaves - 1; L.route = 0; L.sdown_ready = 0; }
-    if (tid < 8) { L.ids[tid] = 0; L.w[tid] = 0.f; L.order[tid] = tid; }
+    {
+        // (an opaque zero: with constants the whole-step kernel kept these
+        // values in registers from its start, through every stage)
+        int z = 0;
+        asm volatile("" : "+v"(z));
+        if (tid == 0) { L.next = kWaves - 1 + z; L.route = z; L.sdown_ready = z; }
+        if (tid < 8) { L.ids[tid] = z; L.w[tid] = (float)z; L.order[tid] = tid; }
+    }
     if constexpr (kMega) {
         // x: every workgroup's published rows (polled behind this wave's first
         // router rows and pair, which are in flight already), or the launch's
@@ -795,6 +820,7 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L) {
         if (lane < 4) L.part[0][rs + lane] = d;
     }
     FLEET_TRACE(6);
+    next();
     __syncthreads();
 
     // a7: bf16(w_k * d_k) summed in exact selection order, then the shared

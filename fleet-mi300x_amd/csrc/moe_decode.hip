@@ -7,7 +7,8 @@ namespace decode {
 
 __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(Params P) {
     __shared__ Lds L;
-    moe_layer<false>(P, L);
+    u32x4 pre[8];
+    moe_layer<false>(P, L, pre, false, [] {});
 }
 
 }  // namespace decode

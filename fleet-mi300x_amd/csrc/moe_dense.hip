@@ -7,7 +7,8 @@ namespace dense {
 
 __global__ __launch_bounds__(kThreads, 1) void dense_kernel(Params P) {
     __shared__ Lds L;
-    dense_layer<false>(P, L);
+    u32x4 pre[8];
+    dense_layer<false>(P, L, pre, false, [] {});
 }
 
 }  // namespace dense

@@ -159,6 +159,11 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     // stage numbering: the decode step's attention of layer i is stage 2i + 1
     // and its FFN 2i + 2; the column's FFN of layer i is stage i + 1. Stage s
     // publishes into xbuf[s % 2] with tag xtag(s) and reads stage s - 1's.
+    // A stage issues the next stage's first loads (an attention's first rows,
+    // a MoE stage's first shared pair per streaming wave) into `pre` once its
+    // own last wait is done, and the next stage starts on them (pre_in).
+    u32x4 pre[8];
+    bool pre_in = false;
     for (int i = 0; i < S.n_layers; ++i) {
         const fleet_step_layer& ly = tbl[i];
         const bool last = i == S.n_layers - 1;
@@ -187,12 +192,34 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
 #if FLEET_STEP_TRACE && FLEET_ATTN_TRACE
             A.trace = i == S.trace_layer ? S.trace_a : nullptr;
 #endif
-            attn::attn_layer<true>(A, L.a);
+            // the FFN of this layer follows: its first pair
+            auto next = [&]() {
+                if (ly.dense) dense::issue_first_pair(ly.dense, pre);
+                else decode::issue_first_pair(ly.moe.shared, pre);
+            };
+            attn::attn_layer<true>(A, L.a, pre, pre_in, next);
+            pre_in = true;
             __syncthreads();
             STEP_TRACE(st);
         }
         const int st = kFull ? 2 * i + 2 : i + 1;
         const bool first = !kFull && i == 0;
+        // the next stage: the attention of layer i + 1 (decode step) or its
+        // FFN (column); after the last layer nothing (the buffer is cleared,
+        // so that no path leaves it holding older values)
+        const fleet_step_layer* nl = last ? nullptr : &tbl[i + 1];
+        auto next = [&]() {
+            if (!nl) {
+#pragma unroll
+                for (int m = 0; m < 8; ++m) pre[m] = u32x4{0u, 0u, 0u, 0u};
+            } else if constexpr (kFull) {
+                attn::issue_first_rows(nl->attn.qkv, pre);
+            } else if (nl->dense) {
+                dense::issue_first_pair(nl->dense, pre);
+            } else {
+                decode::issue_first_pair(nl->moe.shared, pre);
+            }
+        };
         if (ly.dense) {
             dense::Params D{};
             D.norm = ly.moe.norm;
@@ -206,7 +233,7 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             D.xin_tag = xtag(st - 1);
             D.xout = xbuf[st % 2];
             D.xout_tag = xtag(st);
-            dense::dense_layer<true>(D, L.d);
+            dense::dense_layer<true>(D, L.d, pre, pre_in, next);
         } else {
             decode::Params M{};
             M.norm = ly.moe.norm;
@@ -227,8 +254,9 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
 #if FLEET_STEP_TRACE && FLEET_MOE_TRACE
             M.trace = i == S.trace_layer ? S.trace_m : nullptr;
 #endif
-            decode::moe_layer<true>(M, L.m);
+            decode::moe_layer<true>(M, L.m, pre, pre_in, next);
         }
+        pre_in = true;
         __syncthreads();
         STEP_TRACE(st);
     }
