@@ -658,8 +658,13 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
                 __builtin_amdgcn_global_load_lds(src + k * 1024, L.sdown + k * 1024, 16, 0, 0);
         }
         weights_pending = ok && !exact_sel;
-        cur = claim();
-        if (weights_pending) ew = ld_exact_logit(P);
+        // In the whole-step kernel the control wave takes no pairs: its
+        // copies hold its first pair back until ~13 us into the stage, and it
+        // was then the workgroup's last wave to finish phase G in a third of
+        // the workgroups (column 760 -> 750 us/token without it; the
+        // single-layer launch is 0.2 us faster with it).
+        cur = kMega ? -1 : claim();
+        if (weights_pending && cur >= 0) ew = ld_exact_logit(P);
         if (cur >= 0) issue(cur, bufA);
     }
     FLEET_TRACE(2);
