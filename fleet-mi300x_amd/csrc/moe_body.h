@@ -715,25 +715,31 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
                                                 : u32x4{0u, 0u, 0u, 0u};
             }
         FLEET_TRACE(4);
+        // the 8 rows' sums of squares (lane r < 8: row r), while the h this
+        // wave waits for below is still being produced
+        float nv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const u32x4* w = &W[3 * r];
+            nv[r] = (dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) +
+                    dot8_d2(w[2], w[2], 0.f);
+        }
+        const float w2 = wave_nsum(nv);
         u32x4 H[3];
         wait_h<3>(P, unit, kInterChunks, tag, H);
         FLEET_TRACE(5);
         float hv[1] = {(dot8_d2(H[0], H[0], 0.f) + dot8_d2(H[1], H[1], 0.f)) +
                        dot8_d2(H[2], H[2], 0.f)};
         const float hn = __builtin_sqrtf(wave_nsum(hv)) * 1.0001f;
-        // the 8 rows' dots and sums of squares reduced together: lane r < 8
-        // holds row r's dot, lane 8 + r its sum of squares
-        float v[16];
+        // the 8 rows' dots reduced together: lane r < 8 holds row r's
+        float v[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const u32x4* w = &W[3 * r];
             v[r] = (dot8_d2(w[0], H[0], 0.f) + dot8_d2(w[1], H[1], 0.f)) +
                    dot8_d2(w[2], H[2], 0.f);
-            v[8 + r] = (dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) +
-                       dot8_d2(w[2], w[2], 0.f);
         }
         const float s = wave_nsum(v);
-        const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x128));   // lane + 8
         float d;
         const bool ok = certify_bf16(s, w2, hn, cert_gamma(16), d);  // v_dot2 chain 8, tree 2, sum 6
         const uint64_t bad = __ballot(!ok) & 0xffull;
@@ -770,37 +776,47 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
         }
         FLEET_TRACE(4);
         u32x4 H[6];
-        wait_h<6>(P, unit, kSharedChunks, tag, H);
-        FLEET_TRACE(5);
         const int rs = 4 * (wave - kTopK);
-        float hq[6];
-#pragma unroll
-        for (int m = 0; m < 6; ++m) hq[m] = dot8_d2(H[m], H[m], 0.f);
-        float hv[1] = {((hq[0] + hq[1]) + (hq[2] + hq[3])) + (hq[4] + hq[5])};
-        const float hn = __builtin_sqrtf(wave_nsum(hv)) * 1.0001f;
-        // the 4 rows' dots and sums of squares reduced together: lane r < 4
-        // holds row rs + r's dot, lane 4 + r its sum of squares
-        float v[8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        auto srow = [&](int r, u32x4 (&w)[6]) {
             const u32x4* wr = reinterpret_cast<const u32x4*>(L.sdown + (rs + r) * kSharedRowBytes);
-            u32x4 w[6];
 #pragma unroll
             for (int m = 0; m < 6; ++m) {
                 const int c = lane + kLanes * m;
                 w[m] = c < kSharedChunks ? wr[c] : u32x4{0u, 0u, 0u, 0u};
             }
-            float av[6], nv[6];
+        };
+        // the 4 rows' sums of squares (lane r < 4: row rs + r), while the h
+        // this wave waits for below is still being produced
+        float nq[4];
 #pragma unroll
-            for (int m = 0; m < 6; ++m) {
-                av[m] = dot8_d2(w[m], H[m], 0.f);
-                nv[m] = dot8_d2(w[m], w[m], 0.f);
-            }
+        for (int r = 0; r < 4; ++r) {
+            u32x4 w[6];
+            srow(r, w);
+            float nv[6];
+#pragma unroll
+            for (int m = 0; m < 6; ++m) nv[m] = dot8_d2(w[m], w[m], 0.f);
+            nq[r] = ((nv[0] + nv[1]) + (nv[2] + nv[3])) + (nv[4] + nv[5]);
+        }
+        const float w2 = wave_nsum(nq);
+        wait_h<6>(P, unit, kSharedChunks, tag, H);
+        FLEET_TRACE(5);
+        float hq[6];
+#pragma unroll
+        for (int m = 0; m < 6; ++m) hq[m] = dot8_d2(H[m], H[m], 0.f);
+        float hv[1] = {((hq[0] + hq[1]) + (hq[2] + hq[3])) + (hq[4] + hq[5])};
+        const float hn = __builtin_sqrtf(wave_nsum(hv)) * 1.0001f;
+        // the 4 rows' dots reduced together: lane r < 4 holds row rs + r's
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            u32x4 w[6];
+            srow(r, w);
+            float av[6];
+#pragma unroll
+            for (int m = 0; m < 6; ++m) av[m] = dot8_d2(w[m], H[m], 0.f);
             v[r] = ((av[0] + av[1]) + (av[2] + av[3])) + (av[4] + av[5]);
-            v[4 + r] = ((nv[0] + nv[1]) + (nv[2] + nv[3])) + (nv[4] + nv[5]);
         }
         const float s = wave_nsum(v);
-        const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x124));   // lane + 4
         float d;
         const bool ok = certify_bf16(s, w2, hn, cert_gamma(17), d);  // v_dot2 chain 8, tree 3, sum 6
         const uint64_t bad = __ballot(!ok) & 0xfull;
