@@ -124,6 +124,7 @@ struct Params {
     uint32_t xin_tag;
     uint32_t* xout;            // tagged x_out [kXCopies][kHidden]
     uint32_t xout_tag;
+    bool router_first;         // all eight router rows per wave before x (see the prologue)
 #if FLEET_MOE_TRACE
     unsigned long long* trace; // [kWG][kWaves][16] s_memrealtime stamps, or null
 #endif
@@ -497,6 +498,20 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             ra[r][m] = ld_global(P.router + (int64_t)(rrow0 + r) * kRowChunks + lane + kLanes * m);
+    // The second half of the wave's router rows goes out here too in the FFN
+    // column (after an FFN stage x comes late, and the rows are in by the
+    // time it is normed: column 728 -> 721 us/token); otherwise after the
+    // first step of the RMSNorm (after an attention stage, or in a launch of
+    // its own, issuing them here is slower).
+    u32x4 rb[4][4];
+    const bool rb_first = kMega && P.router_first;
+    if (rb_first) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                rb[r][m] = ld_global(P.router + (int64_t)(rrow0 + 4 + r) * kRowChunks + lane + kLanes * m);
+    }
     const bool exact_row = ctl && wg < kRouted;
     u32x4 er[4];
     if (exact_row) {
@@ -554,12 +569,13 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
         if (lane == 0) L.xsq[wave] = qs;
     }
     // the second half of this wave's local router rows
-    u32x4 rb[4][4];
+    if (!rb_first) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            rb[r][m] = ld_global(P.router + (int64_t)(rrow0 + 4 + r) * kRowChunks + lane + kLanes * m);
+            for (int m = 0; m < 4; ++m)
+                rb[r][m] = ld_global(P.router + (int64_t)(rrow0 + 4 + r) * kRowChunks + lane + kLanes * m);
+    }
     __syncthreads();
     u32x4 xq[4];
 #pragma unroll

@@ -251,6 +251,7 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
             M.xin_tag = xtag(st - 1);
             M.xout = xbuf[st % 2];
             M.xout_tag = xtag(st);
+            M.router_first = !kFull;
 #if FLEET_STEP_TRACE && FLEET_MOE_TRACE
             M.trace = i == S.trace_layer ? S.trace_m : nullptr;
 #endif
