@@ -96,6 +96,7 @@ def counter_view(result: dict, profiled: dict) -> dict:
         "lm_head": get("attention", "lm_head", "us"),
         "dense": dense,
         "moe_layer_in_column": (col - dense) / 26 if col and dense else None,
+        "column": col,
     }
     for t in ("T4", "T16", "T64"):
         times[f"grouped_{t}"] = get("grouped", t, "us_per_step")
