@@ -91,10 +91,6 @@ __device__ __forceinline__ void issue_pair(const u32x4* base, int lane, u32x4 (&
     }
 }
 
-// The layer. kMega: inside the whole-step kernel (fleet_decode_step): the
-// call count comes from the step (P.epoch), x from the tagged exchange buffer
-// P.xin and x_out goes to the exchange buffer P.xout (and to P.x_out when
-// that is not null).
 // A wave's first gate/up pair (pair wg + 256 wave, if the workgroup has
 // that many; zeros otherwise), issued into `b`. The whole-step kernel issues
 // it from the stage before this one, once that stage's last wait is done.
@@ -110,9 +106,13 @@ __device__ __forceinline__ void issue_first_pair(const uint16_t* w, u32x4 (&b)[8
     }
 }
 
-// `pre` is the first pair's buffer; with pre_in the pair was issued by the
-// stage before (otherwise here). `next` runs once this layer's last wait is
-// done: the whole-step kernel issues the next stage's first loads there.
+// The layer. kMega: inside the whole-step kernel (fleet_decode_step): the
+// call count comes from the step (P.epoch), x from the tagged exchange buffer
+// P.xin and x_out goes to the exchange buffer P.xout (and to P.x_out when
+// that is not null). `pre` is the first pair's buffer; with pre_in the pair
+// was issued by the stage before (otherwise here). `next` runs once this
+// layer's last wait is done: the whole-step kernel issues the next stage's
+// first loads there.
 template <bool kMega, class Next>
 __device__ __forceinline__ void dense_layer(const Params& P, Lds& L, u32x4 (&pre)[8], bool pre_in,
                                             Next&& next) {

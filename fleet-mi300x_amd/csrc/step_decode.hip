@@ -95,9 +95,6 @@ union Lds {
     attn::HeadLds h;
 };
 
-// kFull: the decode step (embed, attention and FFN of every layer, lm_head,
-// argmax). Otherwise the FFN column: the FFN stage of every layer of the table
-// on S.x_in, the last one's output in S.x_out (no attention, no position).
 // A word written by an earlier launch, read through the scalar cache (which
 // every launch starts with invalidated): a uniform value in SGPRs, its wait
 // independent of the vector loads in flight.
@@ -110,6 +107,9 @@ constexpr int kLayerWords = sizeof(fleet_step_layer) / 8;
 static_assert(sizeof(fleet_step_layer) % 8 == 0, "the layer table is copied in 8-byte words");
 static_assert(kMaxLayers * kLayerWords <= 2 * kThreads, "two table words per thread at most");
 
+// kFull: the decode step (embed, attention and FFN of every layer, lm_head,
+// argmax). Otherwise the FFN column: the FFN stage of every layer of the table
+// on S.x_in, the last one's output in S.x_out (no attention, no position).
 template <bool kFull>
 __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     __shared__ Lds L;
