@@ -153,3 +153,25 @@ def test_attention_entry_points_reject_bad_arguments_without_device(lib):
                                     ctypes.byref(d), None) == _lib.ERR_ARG
     assert lib.fleet_lm_head_argmax(256, None, 256, None, 258, None, None, 256, n,
                                     ctypes.byref(d), None) == _lib.ERR_ARG
+
+
+def test_trace_build_exports_the_library_and_its_trace_hooks():
+    """The stage-trace build (a diagnostic variant of the same sources) binds
+    like the library and adds only its three trace hooks; the library itself
+    has none of them."""
+    from fleet_moe import _build, stage_trace
+    if not stage_trace.TRACE_LIB.exists():
+        pytest.skip("trace build not made (python -m fleet_moe._build --trace)")
+    prev = _lib._LIB
+    try:
+        tl = stage_trace.load()
+        for name, _, _ in _lib.SYMBOLS:
+            assert getattr(tl, name) is not None
+    finally:
+        _lib._LIB = prev
+    lib = _lib.load()
+    for hook in ("fleet_step_debug_set_trace", "fleet_moe_debug_set_trace",
+                 "fleet_attn_debug_set_trace"):
+        assert getattr(tl, hook) is not None
+        assert not hasattr(lib, hook), hook
+    assert _build.TRACE_OUT != _build.OUT
