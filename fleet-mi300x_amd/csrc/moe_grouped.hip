@@ -159,6 +159,7 @@ struct Lds {
     int n_units, g_total, d_total;
     int n_gseg, n_dseg, g_items, d_items;
     int gnext, dnext;
+    int exit_last;                     // this workgroup exits last (the wrap call)
     float red[kWaves][kLanes];
     union {
         alignas(16) uint8_t stage[kStageBytes];          // VALU units: x or h rows
@@ -1057,21 +1058,27 @@ __device__ void combine(const Params& P, uint32_t epoch) {
 // zero-filled word carries), so that workgroup first clears every tagged word
 // and restarts the count from 0, which leaves the workspace as it was when
 // new; the next launch on the stream starts after this one has finished.
-__device__ void exit_epoch(const Params& P, uint32_t epoch) {
-    __shared__ int s_last;
+// (The flag for that call lives in the workgroup's Lds: a __shared__ variable
+// of its own beside it moved the Lds and made the two-launch step's MFMA
+// streaming ~9 us slower at 64 tokens.)
+__device__ void exit_epoch(const Params& P, Lds& L, uint32_t epoch) {
     Header* hdr = P.hdr;
     __syncthreads();
+    if (epoch != 0xffffffffu) {
+        if (threadIdx.x == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(&hdr->exits, 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+            if (old + 1u == epoch * (uint32_t)kWG) st_agent(&hdr->epoch, epoch);
+        }
+        return;
+    }
     if (threadIdx.x == 0) {
         const uint32_t old = __hip_atomic_fetch_add(&hdr->exits, 1u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old + 1u == epoch * (uint32_t)kWG;
+        L.exit_last = old + 1u == epoch * (uint32_t)kWG;
     }
     __syncthreads();
-    if (!s_last) return;
-    if (epoch != 0xffffffffu) {
-        if (threadIdx.x == 0) st_agent(&hdr->epoch, epoch);
-        return;
-    }
+    if (!L.exit_last) return;
     u32x4* w = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(hdr) + sizeof(Header));
     const u32x4 z = {0u, 0u, 0u, 0u};
     for (size_t i = threadIdx.x; i < P.ws_tail16; i += kThreads) w[i] = z;
@@ -1099,7 +1106,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_fused_kernel(Params P) {
     __syncthreads();
     v_items<false>(P, L, epoch);
     combine<false>(P, epoch);
-    exit_epoch(P, epoch);
+    exit_epoch(P, L, epoch);
 }
 
 // T > 8, launch 1: phase G, h as plain words.
@@ -1127,7 +1134,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_dc_kernel(Params P) {
     __syncthreads();
     v_items<false>(P, L, epoch);
     combine<true>(P, epoch);
-    exit_epoch(P, epoch);
+    exit_epoch(P, L, epoch);
 }
 
 }  // namespace grouped
