@@ -91,19 +91,17 @@ __device__ __forceinline__ void issue_pair(const u32x4* base, int lane, u32x4 (&
     }
 }
 
-// A wave's first gate/up pair (pair wg + 256 wave, if the workgroup has
-// that many; zeros otherwise), issued into `b`. The whole-step kernel issues
-// it from the stage before this one, once that stage's last wait is done.
+// A wave's first gate/up pair (pair wg + 256 wave), issued into `b`. The
+// whole-step kernel issues it from the stage before this one, once that
+// stage's last wait is done. Every wave has one (a workgroup has at least 42
+// pairs), and the issue is unconditional: behind a branch, the compiler
+// waited for every load in flight (the pair too) before the RMSNorm read x.
+static_assert(kDenseInter / kWG >= kWaves, "every wave has a first pair");
 __device__ __forceinline__ void issue_first_pair(const uint16_t* w, u32x4 (&b)[8]) {
     const int wg = blockIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(fm_tid() >> 6);
-    if (wave < pairs_of(wg)) {
-        issue_pair(reinterpret_cast<const u32x4*>(w) + (int64_t)(wg + kWG * wave) * 2 * kRowChunks,
-                   fm_tid() & (kLanes - 1), b);
-    } else {
-#pragma unroll
-        for (int m = 0; m < 8; ++m) b[m] = u32x4{0u, 0u, 0u, 0u};
-    }
+    issue_pair(reinterpret_cast<const u32x4*>(w) + (int64_t)(wg + kWG * wave) * 2 * kRowChunks,
+               fm_tid() & (kLanes - 1), b);
 }
 
 // The layer. kMega: inside the whole-step kernel (fleet_decode_step): the
@@ -131,7 +129,7 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L, u32x4 (&pre
     const u32x4* gu = reinterpret_cast<const u32x4*>(P.w);
     const int n_items = pairs_of(wg);
     u32x4 (&buf)[8] = pre;
-    int cur = wave < n_items ? wave : -1;
+    int cur = wave;                           // every wave's first pair (see above)
     if (!(kMega && pre_in)) issue_first_pair(P.w, buf);
     if (tid == 0) L.next = kWaves;
     if constexpr (kMega) {
