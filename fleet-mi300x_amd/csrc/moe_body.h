@@ -690,19 +690,34 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
     // selected set) as soon as they may be published: each poll is issued
     // just before a pair's loads, so the pair's wait covers it and the wave
     // never stalls on it alone.
-    while (cur >= 0) {
-        const int nxt = claim();
-        finish(cur, bufA);
-        if (weights_pending) {
-            if (__all((uint32_t)(ew >> 32) == epoch)) {
-                exact_weights_from(P, L, __uint_as_float((uint32_t)ew));
-                weights_pending = false;
-            } else if (nxt >= 0) {
-                ew = ld_exact_logit(P);
+    // The control wave's loop (it also polls the exact logits) is kept apart
+    // from the streaming waves' loop, and it consumes its last poll before
+    // the paths join: a poll's destination register, possibly still loading
+    // on some path, made the compiler wait for every load in flight before
+    // the routed waves' down rows (vmcnt(0) on reuse of that register).
+    if (ctl) {
+        while (cur >= 0) {
+            const int nxt = claim();
+            finish(cur, bufA);
+            if (weights_pending) {
+                if (__all((uint32_t)(ew >> 32) == epoch)) {
+                    exact_weights_from(P, L, __uint_as_float((uint32_t)ew));
+                    weights_pending = false;
+                } else if (nxt >= 0) {
+                    ew = ld_exact_logit(P);
+                }
             }
+            if (nxt >= 0) issue(nxt, bufA);
+            cur = nxt;
         }
-        if (nxt >= 0) issue(nxt, bufA);
-        cur = nxt;
+        asm volatile("" ::"v"(ew));
+    } else {
+        while (cur >= 0) {
+            const int nxt = claim();
+            finish(cur, bufA);
+            if (nxt >= 0) issue(nxt, bufA);
+            cur = nxt;
+        }
     }
     FLEET_TRACE(3);
 
@@ -722,14 +737,26 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
                                 P.experts + (int64_t)expert * P.expert_stride +
                                 (int64_t)2 * kInter * kHidden) +
                             (int64_t)row0 * kInterChunks;
+        // Every lane loads all 24 chunks: lanes 48..63 read chunk 175 of the
+        // row again for m = 2 (their chunk 176 + would be past the row), and
+        // that copy is left out where it is used (the row norms below; in the
+        // dots h is zero there), so no per-lane condition splits the issue.
+        // The rows go out in three groups, rows 0-1, 2-3, then 4-7, each after
+        // the one before has landed: a workgroup done with phase G early then
+        // leaves more of the memory system to the workgroups still streaming
+        // their pairs, whose h every workgroup waits for (all 24 loads at
+        // once: single layer +0.4 us, column +12 us/token; in three groups:
+        // single layer -0.2 us, column -8 us, decode step -20 us/token).
+        const bool tail = lane + 2 * kLanes < kInterChunks;
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
+        for (int r = 0; r < 8; ++r) {
+            if (r == 2 || r == 4) asm volatile("" ::"v"(W[3 * r - 1].x));   // the group before has landed
 #pragma unroll
             for (int m = 0; m < 3; ++m) {
-                const int c = lane + kLanes * m;
-                W[3 * r + m] = c < kInterChunks ? ld_stream(base + r * kInterChunks + c)
-                                                : u32x4{0u, 0u, 0u, 0u};
+                const int c = m < 2 ? lane + kLanes * m : min(lane + kLanes * m, kInterChunks - 1);
+                W[3 * r + m] = ld_stream(base + r * kInterChunks + c);
             }
+        }
         FLEET_TRACE(4);
         // the 8 rows' sums of squares (lane r < 8: row r), while the h this
         // wave waits for below is still being produced
@@ -737,8 +764,8 @@ __device__ __forceinline__ void moe_layer(const Params& P, Lds& L, u32x4 (&pre)[
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const u32x4* w = &W[3 * r];
-            nv[r] = (dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) +
-                    dot8_d2(w[2], w[2], 0.f);
+            const float t = dot8_d2(w[2], w[2], 0.f);
+            nv[r] = (dot8_d2(w[0], w[0], 0.f) + dot8_d2(w[1], w[1], 0.f)) + (tail ? t : 0.f);
         }
         const float w2 = wave_nsum(nv);
         u32x4 H[3];
