@@ -45,6 +45,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=50, help="tokens per event-timed batch")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget")
+    ap.add_argument("--cpu-tokens", type=int, default=1000,
+                    help="tokens in the CPU baseline's sample (config 1's first N, whatever "
+                         "--steps is), cut short by --cpu-seconds")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true")
     ap.add_argument("--no-cold", action="store_true",
@@ -133,7 +136,8 @@ def cpu_baseline(blob, lay, x_tok: np.ndarray, budget_s: float, gpu_ids: np.ndar
                          shared=view_u16(blob, t["L1.shared"]), expert_stride=orc.HIDDEN * orc.MOE_INTER * 3,
                          norm=view_u16(blob, t["L1.norm_post"]))
     pl.widen()
-    orc.moe_layer_fp32(pl, x_tok[0])                 # warm-up call
+    for i in range(3):                               # warm-up calls (BLAS threads start)
+        orc.moe_layer_fp32(pl, x_tok[i % x_tok.shape[0]])
     times, n_match = [], 0
     t_end = time.perf_counter() + budget_s
     for i in range(x_tok.shape[0]):
@@ -187,7 +191,8 @@ def main() -> int:
     blob, lay = synth.moe_layer_blob(seed=0, layer=1, dims=dims)
     layer = ops.DeviceLayer.from_host(blob, lay, 1, dims, device=dev)
     n_tok = max(args.steps, 1)
-    x_host = bf16_tokens(synth, max(n_tok, args.warmup))
+    n_cpu = 0 if args.no_cpu else max(args.cpu_tokens, 1)
+    x_host = bf16_tokens(synth, max(n_tok, args.warmup, n_cpu))
     xd = torch.from_numpy(x_host).to(dev)
     outs = torch.empty_like(xd)
     ids = torch.empty((xd.shape[0], dims.top_k), dtype=torch.int32, device=dev)
@@ -233,6 +238,11 @@ def main() -> int:
     per_batch = [evs[i].elapsed_time(evs[i + 1]) * 1e3 / B for i in range(nb)]
     total_ms = evs[0].elapsed_time(end_all)
     us_layer = float(np.median(per_batch)) if per_batch else total_ms * 1e3 / K
+    # the GPU's routing of the rest of the CPU baseline's sample (untimed), so
+    # that every CPU token's ids are compared
+    for t in range(K, n_cpu):
+        launch(t)
+    torch.cuda.synchronize()
     status = dec.status()
 
     # Kernel duration: the launches above run back to back on one stream, so
@@ -316,7 +326,8 @@ def main() -> int:
 
     result["counters"] = counter_view(result, profiled)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(blob, lay, x_host[:K], args.cpu_seconds, gpu_ids)
+        result["cpu_baseline"] = cpu_baseline(blob, lay, x_host[:n_cpu], args.cpu_seconds,
+                                              gpu_ids)
     print(json.dumps(result), flush=True)
     return 0 if status == 0 else 1
 

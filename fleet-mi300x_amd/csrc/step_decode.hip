@@ -33,7 +33,16 @@ namespace step {
 
 constexpr int kWG = 256;
 constexpr int kThreads = 512;
-constexpr int kMaxLayers = 64;
+constexpr int kMaxLayers = FLEET_STEP_MAX_LAYERS;
+// Residual exchange tags advance by kTagStride per step. A step has stages
+// 1 .. 2 n_layers (and the lm_head reads stage 2 n_layers), so the stride must
+// exceed every stage number: a buffer polled at stage s of step k then holds
+// either stage s - 2 of step k or the last stage of its parity of step k - 1,
+// and neither can carry step k's tag for stage s - 1 (with a stride of 64, a
+// 33-layer step's stage 2 read step k - 1's stage 65 as current).
+constexpr uint32_t kTagStride = 256;
+static_assert(kTagStride >= 2 * kMaxLayers + 2, "a step's stages must fit in its tag stride");
+static_assert(65536 % kTagStride == 0, "16-bit tags: consecutive steps never share a tag");
 static_assert(attn::kWG == kWG && decode::kWG == kWG && dense::kWG == kWG, "one grid");
 static_assert(attn::kThreads == kThreads && decode::kThreads == kThreads &&
                   dense::kThreads == kThreads,
@@ -143,8 +152,8 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
     const uint32_t ea = kFull ? ld_launch_const(&S.aws->epoch) : 0u;
     const uint32_t em = ld_launch_const(&S.mws->epoch), ed = ld_launch_const(&S.dws->epoch),
                    es = ld_launch_const(&S.sws->epoch);
-    // exchange tags: 64 per step (2 per layer), so consecutive steps differ
-    const uint32_t sbase = (es + 1u) * 64u;
+    // exchange tags: kTagStride per step, one per stage
+    const uint32_t sbase = (es + 1u) * kTagStride;
     auto xtag = [&](int stage) { return ((sbase + (uint32_t)stage) & 0xffffu) << 16; };
     uint32_t* xbuf[2] = {&S.sws->x[0][0][0], &S.sws->x[1][0][0]};
     int n_moe = 0, n_dense = 0;
@@ -276,6 +285,13 @@ __global__ __launch_bounds__(kThreads, 1) void step_kernel(Params S) {
         H.pos_advance = S.pos_dev;
         attn::lmhead_body<true>(H, L.h);
         STEP_TRACE(2 * S.n_layers + 1);
+    } else if (S.n_layers == 1) {
+        // A one-layer column writes only xbuf[1]. Stamp xbuf[0] with this
+        // step's stage-0 tag, which no stage polls, so that neither buffer
+        // ever holds words older than the previous step (a 16-bit tag comes
+        // back every 65536 / kTagStride steps).
+        const int g = wg * kThreads + tid;
+        if (g < kXCopies * kHidden) st_agent(xbuf[0] + g, xtag(0));
     }
     // workgroup 0 advances the call counts: the argmax (decode step) or the
     // last FFN stage's h exchange (column) needed every workgroup, so every

@@ -1,9 +1,11 @@
 """fleet_moe: MI355X-native batch-1 MoE decode path for DeepSeek-V2-Lite.
 
 Python host side over the C ABI of libfleet_moe.so (include/fleet_moe.h):
-`layout` (packed-weight layout and manifest), `synth` (seeded synthetic
-weights), `ops` (device buffers and calls), `taskgraph` (the reference's
-64-byte task descriptors for the MoE task kinds).
+`layout` (packed-weight layout and manifest), `hf_pack` (a local HF
+checkpoint into that layout), `synth` / `synth_gpu` (seeded synthetic weights
+on the host / device), `rope` (the YaRN rotary tables), `ops` (device buffers
+and calls), `descriptors` (the reference's 64-byte task descriptors: the MoE
+task kinds planned onto library calls).
 """
 from .layout import DSV2_LITE, MoeDims  # noqa: F401
 

@@ -249,9 +249,13 @@ typedef struct fleet_step_layer {
     uint16_t* cache;
 } fleet_step_layer;
 
-/* The model: layers is a DEVICE array of n_layers (<= 64) entries, which the
- * kernel reads; embed, lm_head bf16 [102400][hidden]; final_norm bf16[hidden]
- * or NULL; rope_cos / rope_sin fp32 [max_pos][64], max_pos <= 4096. */
+/* Most layers a fleet_decode_step / fleet_ffn_column layer table may hold. */
+#define FLEET_STEP_MAX_LAYERS 64
+
+/* The model: layers is a DEVICE array of n_layers (<= FLEET_STEP_MAX_LAYERS)
+ * entries, which the kernel reads; embed, lm_head bf16 [102400][hidden];
+ * final_norm bf16[hidden] or NULL; rope_cos / rope_sin fp32 [max_pos][64],
+ * max_pos <= 4096. */
 typedef struct fleet_step_model {
     const fleet_step_layer* layers;
     int32_t n_layers;

@@ -5,17 +5,17 @@ vocabulary cut to 3 layers (dense layer 0, MoE layers 1-2) so the oracle
 finishes in seconds. Weights are drawn on the device (synth_gpu.fill_model)
 and read back for the oracle.
 
-Checked:
+Every kernel on this path rounds exactly as the oracle does (each dot
+product's exact value rounded once, fp64 norms and softmax), so every check is
+bit-equality:
 * teacher-forced through the whole stack: after the GPU prefill, one step at
   the next position is run layer by layer and the oracle gets the GPU's input
   of every layer and the GPU's cache; every layer's attention half, FFN half
-  and appended cache row within bf16 tolerance (rel 1e-2, >= 95% of elements
-  bit-equal), the logits likewise and the same token;
+  and appended cache row, and the logits, bit-equal, and the same token;
 * free-running: the GPU prefills a seeded uniform prompt and generates
   greedily from its own state, the oracle does the same from its own; the
-  greedy tokens are identical (the top-2 logit margins are printed); the two
-  prefilled caches agree to a few bf16 ulps (rel 5e-2; their states drift by
-  single ulps layer over layer, so only layer 0's rows stay bit-equal);
+  two prefilled caches are bit-equal in every layer and the greedy tokens are
+  identical (the top-2 logit margins are printed);
 * the eager launches and the replayed HIP graph are bit for bit equal
   (caches and tokens)."""
 from __future__ import annotations
@@ -95,9 +95,12 @@ def run_gpu(dec: ops.Decoder, prompt: np.ndarray):
     return tok0, toks, cache
 
 
-def close(got, want, what: str) -> None:
-    assert rel_err(got, want) <= 1e-2, what
-    assert np.mean(got == want) > 0.95, f"{what}: {np.mean(got == want):.3f} bit-equal"
+def same(got, want, what: str) -> None:
+    """Bit-equal fp32 arrays (the message gives the size of any difference)."""
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    assert got.shape == want.shape, what
+    eq = got.view(np.uint32) == want.view(np.uint32)
+    assert eq.all(), (f"{what}: {np.mean(eq):.4f} bit-equal, rel err {rel_err(got, want):.2e}")
 
 
 def test_stack_teacher_forced_matches_oracle(decoder):
@@ -120,20 +123,20 @@ def test_stack_teacher_forced_matches_oracle(decoder):
         dec.attn.attn_into(dec.attn_layers[i], x, x1, dec.cache[i], pos, None, dec.cos, dec.sin)
         dec.ffn.layer_into(i, x1, x)
         r = orc.decoder_layer(m.attn[i], m.ffn[i], x_in, cache_i, pos, cos, sin)
-        close(x1.cpu().numpy(), r["x_attn"], f"layer {i} attention half")
+        same(x1.cpu().numpy(), r["x_attn"], f"layer {i} attention half")
         row = orc.bf16_to_f32(dec.cache[i, pos].cpu().numpy().view(np.uint16))
-        close(row, cache_i[pos], f"layer {i} cache row")
+        same(row, cache_i[pos], f"layer {i} cache row")
         if r["ids"] is not None:
             # the FFN input is the GPU's x1, re-run for the routing comparison
             rr = orc.moe_layer(m.ffn[i], x1.cpu().numpy())
-            close(x.cpu().numpy(), rr["x_out"], f"layer {i} MoE half")
+            same(x.cpu().numpy(), rr["x_out"], f"layer {i} MoE half")
         else:
-            close(x.cpu().numpy(), r["x_out"], f"layer {i} dense half")
+            same(x.cpu().numpy(), r["x_out"], f"layer {i} dense half")
     logits = torch.empty(V, dtype=torch.float32, device="cuda")
     out = torch.empty(1, dtype=torch.int32, device="cuda")
     dec.attn.lm_head_into(x, dec._addr("final_norm"), dec._addr("lm_head"), logits, out)
     r = orc.lm_head_argmax(x.cpu().numpy(), m.final_norm, m.lm_head)
-    close(logits.cpu().numpy(), r["logits"], "logits")
+    same(logits.cpu().numpy(), r["logits"], "logits")
     say(f"token {int(out.item())} (oracle {r['token']}, margin {r['margin']:.4f})")
     assert int(out.item()) == r["token"]
     assert dec.status() == 0
@@ -156,11 +159,7 @@ def test_greedy_decode_matches_oracle(decoder):
     want_toks, margins = [r["token"]], [r["margin"]]
     g_cache = orc.bf16_to_f32(cache.cpu().numpy().view(np.uint16))
     for i in range(dec.n_layers):
-        o = caches[i][:PROMPT]
-        say(f"cache layer {i}: rel err {rel_err(g_cache[i], o):.2e}, "
-            f"bit-equal {np.mean(g_cache[i] == o):.3f}")
-        assert rel_err(g_cache[i], o) <= 5e-2, f"cache layer {i}"
-    assert np.mean(g_cache[0] == caches[0][:PROMPT]) > 0.95
+        same(g_cache[i], caches[i][:PROMPT], f"prefilled cache, layer {i}")
     say("oracle generate")
     for j in range(GEN):
         r = orc.decode_step(m, want_toks[-1], PROMPT + j, caches, cos, sin)

@@ -85,19 +85,22 @@ def test_residual_fold_matches_oracle():
         np.testing.assert_array_equal(xd.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("name", ["default", "local_fold", "oproj_row_split"])
+@pytest.mark.parametrize("name", ["default", "local_fold", "oproj_row_split", "topk_published",
+                                  "split_workers_18"])
 def test_reference_graph_moe_layers_match_the_chained_oracle(two_layers, name):
     dev, pls = two_layers
     descs, events = load(name)
     steps = D.plan(descs, events=events)
-    assert [s.layer for s in steps if isinstance(s, D.MoeCall)] == [1, 2]
+    calls = [s for s in steps if isinstance(s, D.MoeCall)]
+    assert [c.layer for c in calls] == [1, 2]
+    row_split = name == "oproj_row_split"
+    assert all(c.fold_oproj == (not row_split) for c in calls)
     rng = np.random.default_rng(17)
     x_layer1 = orc.bf16_round(rng.standard_normal(H, dtype=np.float32))
     partials = {L: (0.2 * rng.standard_normal((8, H))).astype(np.float32) for L in (1, 2)}
     x0 = torch.zeros(H, dtype=torch.float32, device="cuda")     # Activations.x[0]
     x1 = torch.zeros(H, dtype=torch.float32, device="cuda")     # Activations.x[1]
     op = torch.zeros((8, H), dtype=torch.float32, device="cuda")  # oproj_partial
-    row_split = name == "oproj_row_split"
     seen = []
 
     def runtime_stand_in(seg: D.Segment):

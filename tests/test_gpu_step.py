@@ -7,7 +7,9 @@ times with other work between the replays.
 A 4-layer model (dense layer 0, MoE layers 1-3) with non-unit RMSNorm weights
 on every norm (norm_in, kv_a_norm, norm_post, final_norm), so every weight
 the fused stages read is exercised; 24 teacher-forced steps from position 0,
-then 8 greedy steps."""
+then 8 greedy steps. The same comparison runs on 33- and 64-layer tables that
+reuse those weights, so the residual exchange's tags are exercised at every
+depth where a step has more than 64 stages."""
 from __future__ import annotations
 
 import ctypes
@@ -47,9 +49,10 @@ def model():
     return blob, lay
 
 
-def run(dec: ops.Decoder, prompt: torch.Tensor, use_graph: bool):
-    """PROMPT teacher-forced steps from position 0, then GEN greedy steps;
-    per step the final residual and the pick, then the cache."""
+def run(dec: ops.Decoder, prompt: torch.Tensor, use_graph: bool, n_prompt: int = PROMPT,
+        n_gen: int = GEN):
+    """n_prompt teacher-forced steps from position 0, then n_gen greedy
+    steps; per step the final residual and the pick, then the cache."""
     dec.reset(0)
     xs, picks = [], []
 
@@ -61,15 +64,15 @@ def run(dec: ops.Decoder, prompt: torch.Tensor, use_graph: bool):
         xs.append(dec.x.clone())
         picks.append(dec.token_out.clone())
 
-    for p in range(PROMPT):
+    for p in range(n_prompt):
         dec.token.copy_(prompt[p:p + 1])
         one()
     dec.token.copy_(dec.token_out)
-    for _ in range(GEN):
+    for _ in range(n_gen):
         one()
     torch.cuda.synchronize()
     return (torch.stack(xs).view(torch.int32).cpu(), torch.cat(picks).cpu(),
-            dec.cache[:, :PROMPT + GEN].cpu())
+            dec.cache[:, :n_prompt + n_gen].cpu())
 
 
 def test_fused_step_equals_separate_launches(model):
@@ -96,6 +99,41 @@ def test_fused_step_equals_separate_launches(model):
         torch.cuda.synchronize()
     assert fused.status() == 0
     say(f"{PROMPT + GEN} fused steps equal the separate launches bit for bit")
+
+
+def aliased_layout(lay, n_layers: int):
+    """A layout of n_layers whose layer i reads the drawn layer i (i < LAYERS)
+    or MoE layer 1 + (i - 1) % (LAYERS - 1): deep tables without more
+    weights. Every layer keeps its own KV cache."""
+    fake = lay_mod.Layout(tensors=dict(lay.tensors), scalars=dict(lay.scalars), pos=lay.pos)
+    for i in range(LAYERS, n_layers):
+        src = 1 + (i - 1) % (LAYERS - 1)
+        for name, t in lay.tensors.items():
+            if name.startswith(f"L{src}."):
+                fake.tensors[f"L{i}." + name.split(".", 1)[1]] = t
+    fake.scalars["layers"] = n_layers
+    return fake
+
+
+@pytest.mark.parametrize("n_layers", [33, 64])
+def test_fused_step_equals_separate_launches_on_deep_tables(model, n_layers):
+    """33 layers is the smallest table whose stages (2n + 1 > 64) outran the
+    old per-step tag stride: the first stages of a step then took the
+    previous step's residual as current. 64 is the bound."""
+    blob, lay = model
+    deep = aliased_layout(lay, n_layers)
+    prompt = torch.from_numpy(
+        np.random.default_rng(6).integers(0, lay_mod.VOCAB, 6).astype(np.int32)).cuda()
+    sep = ops.Decoder(blob, deep, DSV2_LITE, max_pos=16, fused=False)
+    fused = ops.Decoder(blob, deep, DSV2_LITE, max_pos=16, fused=True)
+    say(f"{n_layers} layers: separate launches, then one launch per step")
+    x0, p0, c0 = run(sep, prompt, use_graph=False, n_prompt=6, n_gen=4)
+    x1, p1, c1 = run(fused, prompt, use_graph=False, n_prompt=6, n_gen=4)
+    assert sep.status() == 0 and fused.status() == 0
+    assert torch.equal(x0, x1), "final residuals differ"
+    assert torch.equal(c0, c1), "KV caches differ"
+    assert torch.equal(p0, p1), "picks differ"
+    say(f"picks {p1.tolist()}")
 
 
 def test_fused_step_rejects_a_bad_position_without_running(model):
