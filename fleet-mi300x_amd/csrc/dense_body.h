@@ -279,8 +279,11 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L, u32x4 (&pre
         hq[i] = dot8_d2(hv, hv, 0.f);
     }
     // the three sums reduced together: lane % 4 = 0, 1, 2 holds the dot,
-    // the row's and h's sums of squares; every lane of a quad takes all three
-    // (the same bits in every quad, so every lane decides alike)
+    // the row's and h's sums of squares; every lane of a quad takes all three.
+    // Quads can hold different roundings of the same sum (wave_nsum), so the
+    // decision is lane 0's (lane 0 writes the row) and the wave follows it:
+    // decided per lane, a wave split near the bound ran the fp64 fallback
+    // with lanes masked off, and its wave sum missed their terms.
     float v4[4] = {tree_sum(av), tree_sum(wv), tree_sum(hq), 0.f};
     const float s = wave_nsum(v4);
     const float w2 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x55));   // quad lane 1
@@ -288,7 +291,8 @@ __device__ __forceinline__ void dense_layer(const Params& P, Lds& L, u32x4 (&pre
     const float a0 = __int_as_float(FLEET_DPP(__float_as_int(s), 0x00));   // quad lane 0
     const float hn = __builtin_sqrtf(h2) * 1.0001f;
     float out;
-    if (!certify_bf16(a0, w2, hn, cert_gamma(8 + tree_depth(kDnIters) + 6), out)) {
+    const bool okc = certify_bf16(a0, w2, hn, cert_gamma(8 + tree_depth(kDnIters) + 6), out);
+    if (__ballot(!okc) & 1ull) {
         double acc = 0.0;
 #pragma unroll
         for (int i = 0; i < kDnIters; ++i) acc = dot8_x(W[i], h_chunk(i), acc);

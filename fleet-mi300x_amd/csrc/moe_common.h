@@ -226,7 +226,12 @@ __device__ __forceinline__ float xor32_sum(float v) {
 // of the row once). The remaining levels add the single value the same way,
 // then across rows and halves. N sums cost about 3N + 10 instructions
 // instead of N full reductions, and each result is a binary tree of 63 fp32
-// additions, six roundings deep.
+// additions, six roundings deep. For N >= 8 every lane holding a value gets
+// the same tree; for N <= 4 the single-value level on the rotate by 4 pairs
+// lanes asymmetrically (lane l takes (a_l + a_l-4) + (a_l-8 + a_l-12), lane
+// l + 4 takes (a_l+4 + a_l) + (a_l-4 + a_l-8)), so lanes holding the same sum
+// may differ in its last bit: a branch on a result must follow one lane's
+// value (__ballot / readlane), never each lane's own.
 template <int K, int N>
 __device__ __forceinline__ void nsum_level(float (&v)[N], int lane) {
     constexpr int kCtrl = K == 0 ? 0xB1 : K == 1 ? 0x4E : K == 2 ? 0x124 : 0x128;
