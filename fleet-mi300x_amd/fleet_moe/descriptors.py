@@ -394,40 +394,128 @@ class MoeSteps:
                 raise RuntimeError("plan has graph segments but no segment_runner")
 
 
-def moe_layer_descriptors(layer: int, wait_event: int, first_event: int, top_k: int = 6,
-                          n_xcds: int = N_XCDS, workers: int = 37,
-                          oproj_row_split: bool = False) -> tuple[list[Descriptor], int]:
-    """Descriptors of one MoE layer in the reference's shape (a router task per
-    XCD, then gate_up and down per XCD with slot = xcd for xcd < top_k, else a
-    shared half -1, -2), with fresh event ids from `first_event`. Returns the
-    descriptors and the id of the layer's completion event (its last id). Used
-    to build graphs for tests and for callers that emit their own lists."""
+WORKERS_PER_XCD = 37       # worker workgroups per XCD of the reference runtime
+WAVES_PER_WORKER = 4       # its waves per workgroup (producers of a K-chunk event)
+EXPERT_K_CHUNK = 2048      # rows of h per gate_up -> down event (>= moe_inter: one chunk)
+
+
+@dataclass
+class LayerEmit:
+    """One emitted MoE layer: its descriptors (finalized), the events it
+    created (in id order, for the `.events.txt` sidecar) and the id of the
+    event the next layer waits on."""
+    descriptors: list[Descriptor]
+    events: list[Event]
+    done_event: int
+
+
+def emit_moe_layer(layer: int, wait_event, first_event: int, first_index: int = 0, *,
+                   wait_scope: int = Scope.GLOBAL, wait_count: int = N_XCDS * WORKERS_PER_XCD,
+                   top_k: int = 6, moe_inter: int = 1408, k_chunk: int = EXPERT_K_CHUNK,
+                   n_xcds: int = N_XCDS, workers: int = WORKERS_PER_XCD,
+                   waves: int = WAVES_PER_WORKER, topk_published: bool = False,
+                   split_workers: int = 0, oproj_row_split: bool = False,
+                   router_flags: int = 0) -> LayerEmit:
+    """The descriptors of one MoE layer as the reference's emitter writes them
+    (taskgraph.py:366-441, then finalize :500-523), for a caller that builds
+    its own task list around this library's MoE calls or checks a graph.
+
+    Events, from `first_event` on: per XCD the router event `L{l}.norm.x{x}`
+    (XCD-local, one producer per worker) and, with `topk_published`, the
+    top-k publication `L{l}.topk.x{x}`; per XCD the K-chunk events
+    `L{l}.gate_up.x{x}.k{c}` (XCD-local, one producer per wave of the gate_up
+    workers; ceil(moe_inter / k_chunk) of them, consecutive ids); then the
+    layer's GLOBAL `L{l}.down` (one producer per down worker and XCD).
+    Descriptors, from `first_index` on, one per worker of each XCD's chiplet
+    task: NORM_ROUTER, then EXPERT_GATE_UP, then EXPERT_DOWN, the expert slot
+    of XCD x being x for x < top_k and -(x - top_k + 1) (a shared half) after.
+    `split_workers` G > 0 puts gate_up on workers [0, G) and down on [G,
+    workers) of every XCD (WORKER_GROUP; head = the group's first worker,
+    n_split = its size); otherwise down carries ROUTING_CACHED.
+    `wait_event` is what the router tasks wait on: one id, or one per XCD
+    (the --local-fold per-XCD folds, whose `router_flags` add LOCAL_FOLD),
+    with that event's `wait_scope` and `wait_count`. finalize's fields are
+    filled in: every waiter carries its event's scope and producer count,
+    every signaller the count of its event's producers on its own XCD."""
+    waits = list(wait_event) if isinstance(wait_event, (list, tuple)) else [wait_event] * n_xcds
+    if len(waits) != n_xcds:
+        raise ValueError(f"{len(waits)} wait events for {n_xcds} XCDs")
+    if not 0 <= split_workers < workers:
+        raise ValueError(f"split_workers {split_workers} outside [0, {workers})")
+    events: list[Event] = []
+
+    def new_event(scope, producers, label) -> int:
+        events.append(Event(first_event + len(events), int(scope), int(producers), label))
+        return events[-1].id
+
+    n_chunks = -(-moe_inter // k_chunk)
+    G = split_workers
+    gu_group = list(range(G)) if G else list(range(workers))
+    dn_group = list(range(G, workers)) if G else list(range(workers))
+    e_router, e_pub = [], []
+    for x in range(n_xcds):
+        e_router.append(new_event(Scope.XCD_LOCAL, workers, f"L{layer}.norm.x{x}"))
+        e_pub.append(new_event(Scope.XCD_LOCAL, workers, f"L{layer}.topk.x{x}")
+                     if topk_published else -1)
+    e_chunk0 = []
+    for x in range(n_xcds):
+        ids = [new_event(Scope.XCD_LOCAL, len(gu_group) * waves, f"L{layer}.gate_up.x{x}.k{c}")
+               for c in range(n_chunks)]
+        e_chunk0.append(ids[0])
+    e_down = new_event(Scope.GLOBAL, n_xcds * len(dn_group), f"L{layer}.down")
+    by_id = {e.id: e for e in events}
+
+    def slot_of(x: int) -> int:
+        return x if x < top_k else -(x - top_k + 1)
+
+    read = Flags.TOPK_READ if topk_published else Flags.NONE
     out: list[Descriptor] = []
-    ev = first_event
-    routed = []
+
+    def add(kind, x, group, split, **kw):
+        extra = {}
+        if split:
+            extra = {"flags": kw.pop("flags") | Flags.WORKER_GROUP, "head": group[0],
+                     "n_split": len(group)}
+        for w in group:
+            out.append(Descriptor(int(kind), layer, x, w, index=first_index + len(out),
+                                  **{**kw, **extra}))
+
+    def internal_wait(e: int) -> dict:
+        ev = by_id[e]
+        return {"wait_event": e, "wait_scope": ev.scope, "wait_count": ev.producers}
+
+    nr = (Flags.TOPK_PUBLISH if topk_published else Flags.NONE) | \
+         (Flags.OPROJ_ROW_SPLIT if oproj_row_split else Flags.NONE) | Flags(router_flags)
     for x in range(n_xcds):
-        out.append(Descriptor(TaskKind.NORM_ROUTER, layer, x, wait_event=wait_event,
-                              signal_event=ev, signal_scope=Scope.XCD_LOCAL,
-                              n_split=workers,
-                              flags=Flags.OPROJ_ROW_SPLIT if oproj_row_split else Flags.NONE))
-        routed.append(ev)
-        ev += 1
-    chunk = []
+        add(TaskKind.NORM_ROUTER, x, list(range(workers)), False, wait_event=waits[x],
+            wait_scope=int(wait_scope), wait_count=int(wait_count),
+            signal_event=e_router[x], signal_scope=int(Scope.XCD_LOCAL), n_split=workers,
+            local_event=e_pub[x], flags=int(nr), signal_xcd_count=workers)
     for x in range(n_xcds):
-        slot = x if x < top_k else -(x - top_k + 1)
-        out.append(Descriptor(TaskKind.EXPERT_GATE_UP, layer, x, wait_event=routed[x],
-                              expert_slot=slot, local_event=ev, kv_chunk=1,
-                              flags=Flags.CHUNK_SIGNAL))
-        chunk.append(ev)
-        ev += 1
-    done = ev
+        add(TaskKind.EXPERT_GATE_UP, x, gu_group, bool(G), **internal_wait(e_router[x]),
+            expert_slot=slot_of(x), local_event=e_chunk0[x], kv_chunk=n_chunks,
+            flags=int(Flags.CHUNK_SIGNAL | read))
+    dn_flags = Flags.CHUNK_WAIT | read | (Flags.NONE if G else Flags.ROUTING_CACHED)
     for x in range(n_xcds):
-        slot = x if x < top_k else -(x - top_k + 1)
-        out.append(Descriptor(TaskKind.EXPERT_DOWN, layer, x, wait_event=chunk[x],
-                              signal_event=done, signal_scope=Scope.GLOBAL,
-                              expert_slot=slot, local_event=chunk[x], kv_chunk=1,
-                              flags=Flags.CHUNK_WAIT | Flags.ROUTING_CACHED))
-    return out, done
+        add(TaskKind.EXPERT_DOWN, x, dn_group, bool(G), **internal_wait(e_chunk0[x]),
+            signal_event=e_down, signal_scope=int(Scope.GLOBAL), expert_slot=slot_of(x),
+            local_event=e_chunk0[x], kv_chunk=n_chunks, flags=int(dn_flags),
+            signal_xcd_count=len(dn_group))
+    return LayerEmit(out, events, e_down)
+
+
+def moe_layer_descriptors(layer: int, wait_event: int, first_event: int, top_k: int = 6,
+                          n_xcds: int = N_XCDS, workers: int = WORKERS_PER_XCD,
+                          oproj_row_split: bool = False) -> tuple[list[Descriptor], int]:
+    """emit_moe_layer's descriptors and done event (indices from 0)."""
+    e = emit_moe_layer(layer, wait_event, first_event, top_k=top_k, n_xcds=n_xcds,
+                       workers=workers, oproj_row_split=oproj_row_split)
+    return e.descriptors, e.done_event
+
+
+def events_text(events) -> str:
+    """The `.events.txt` sidecar of `events` (taskgraph.py:832-839 grammar)."""
+    return "".join(f"{e.id} {e.scope} {e.producers} {e.label}\n" for e in events)
 
 
 def field_offsets() -> dict[str, int]:
@@ -441,4 +529,6 @@ def field_offsets() -> dict[str, int]:
 
 __all__ = ["DESCRIPTOR_BYTES", "FIELD_NAMES", "TaskKind", "Flags", "Scope", "Descriptor",
            "Event", "MoeLayer", "PlanError", "Segment", "MoeCall", "MoeSteps", "pack_all", "unpack_all",
-           "parse_events", "plan", "moe_layer_descriptors", "field_offsets"]
+           "parse_events", "plan", "LayerEmit", "emit_moe_layer", "moe_layer_descriptors",
+           "events_text", "field_offsets", "WORKERS_PER_XCD", "WAVES_PER_WORKER",
+           "EXPERT_K_CHUNK"]

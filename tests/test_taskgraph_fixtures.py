@@ -120,3 +120,60 @@ def test_plan_refuses_an_unknown_fold_of_expert_partials():
     bad = [replace(d, head=2) if d is r else d for d in descs]
     with pytest.raises(D.PlanError, match="cannot be mapped"):
         D.plan(bad)
+
+
+# ---------------------------------------------------------------- the emit side
+
+EMIT_CFG = {
+    "default": {},
+    "topk_published": {"topk_published": True},
+    "split_workers_18": {"split_workers": 18},
+    "oproj_row_split": {"oproj_row_split": True},
+    "local_fold": {"router_flags": int(F.LOCAL_FOLD)},
+}
+
+
+@pytest.mark.parametrize("name", VARIANTS)
+@pytest.mark.parametrize("layer", [1, 2])
+def test_emitted_moe_layer_equals_the_reference_emitters(name, layer):
+    """emit_moe_layer writes, field for field, the MoE layer the reference's
+    taskgraph.py wrote into the fixture: the same descriptors in the same
+    order with the same indices, and the same events (id, scope, producer
+    count, label) in the sidecar. Where the layer starts (first index, first
+    event id) and what its routers wait on are read from the fixture."""
+    descs, events = load(name)
+    moe = [d for d in descs if d.layer == layer and d.kind in D.MOE_KINDS]
+    lo, hi = moe[0].index, moe[-1].index
+    assert [d.index for d in moe] == list(range(lo, hi + 1)), "contiguous in the stream"
+    mine = [e for e in events if e.label.startswith(f"L{layer}.")
+            and e.label.split(".")[1] in ("norm", "topk", "gate_up", "down")]
+    routers = [d for d in moe if d.kind == K.NORM_ROUTER]
+    waits = [next(d.wait_event for d in routers if d.xcd == x) for x in range(8)]
+    if len(set(waits)) == 1:
+        waits = waits[0]
+    got = D.emit_moe_layer(layer, waits, mine[0].id, lo, wait_scope=routers[0].wait_scope,
+                           wait_count=routers[0].wait_count, **EMIT_CFG[name])
+    assert len(got.descriptors) == len(moe)
+    for g, w in zip(got.descriptors, moe):
+        assert g == w, f"{name} L{layer} index {w.index}:\n got  {g}\n want {w}"
+    assert got.events == mine
+    assert got.done_event == next(e.id for e in mine if e.label == f"L{layer}.down")
+    assert D.events_text(got.events) == "".join(
+        f"{e.id} {e.scope} {e.producers} {e.label}\n" for e in mine)
+
+
+def test_emitted_layer_round_trips_through_the_planner():
+    """A graph whose MoE layer is emitted here plans into one MoE call with
+    the emitted done event, and its consumer loses FOLD_PARTIALS."""
+    lay = D.emit_moe_layer(1, wait_event=0, first_event=1, first_index=1)
+    head = D.Descriptor(int(K.O_PROJ), 1, 0, 0, signal_event=0, signal_scope=int(D.Scope.GLOBAL),
+                        index=0)
+    tail = D.Descriptor(int(K.LM_HEAD), -1, 0, 0, wait_event=lay.done_event,
+                        wait_scope=int(D.Scope.GLOBAL), wait_count=8 * 37,
+                        flags=int(F.FOLD_PARTIALS), index=1 + len(lay.descriptors))
+    stream = D.unpack_all(D.pack_all([head] + lay.descriptors + [tail]))
+    steps = D.plan(stream, events=[D.Event(0, 2, 1, "L1.oproj")] + lay.events)
+    calls = [s for s in steps if isinstance(s, D.MoeCall)]
+    assert len(calls) == 1 and calls[0].source.done_event == lay.done_event
+    last = [s for s in steps if isinstance(s, D.Segment)][-1].descriptors
+    assert last[0].kind == K.LM_HEAD and not last[0].flags & F.FOLD_PARTIALS
