@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import os
 import platform
@@ -69,14 +70,39 @@ def parse_args():
 COUNTERS = ROOT / "profiles" / "kernel_counters.json"
 
 
+def csrc_digest() -> str:
+    """First 16 hex digits of the SHA-256 over the device sources (every file
+    of fleet-mi300x_amd/csrc and include/fleet_moe.h, by name and content):
+    the counter file records the digest of the sources it was measured on."""
+    h = hashlib.sha256()
+    files = sorted((ROOT / "fleet-mi300x_amd" / "csrc").iterdir()) + [ROOT / "include" / "fleet_moe.h"]
+    for f in files:
+        if f.is_file():
+            h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()[:16]
+
+
+def load_counter_file() -> dict:
+    try:
+        return json.loads(COUNTERS.read_text())
+    except (OSError, ValueError):
+        return {}
+
+
 def load_counters() -> dict:
     """Per-leg HBM bytes and MFMA busy cycles per launch or step, from the
     committed rocprofv3 counter passes (FETCH_SIZE / WRITE_SIZE calibrated
     against known-size kernels, SQ_VALU_MFMA_BUSY_CYCLES)."""
-    try:
-        return json.loads(COUNTERS.read_text())["kernels"]
-    except (OSError, ValueError, KeyError):
-        return {}
+    return load_counter_file().get("kernels", {})
+
+
+def counters_source() -> dict:
+    """Which sources the committed counters were measured on, and whether
+    they are the sources of this run."""
+    meas = load_counter_file().get("csrc_sha16")
+    cur = csrc_digest()
+    return {"file": "profiles/kernel_counters.json", "measured_csrc_sha16": meas,
+            "current_csrc_sha16": cur, "matches_current_sources": meas == cur}
 
 
 def counter_view(result: dict, profiled: dict) -> dict:
@@ -281,6 +307,7 @@ def main() -> int:
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_source": counters_source(),
             "kernel": "fleet_moe::decode::moe_decode_kernel",
             "kernel_us_mean": round(k_mean, 3),
             "kernel_us_batch_min": round(float(min(per_batch)), 3) if per_batch else None,
