@@ -131,6 +131,39 @@ def test_attention_layer_matches_oracle(attn_setup):
                                       err_msg=f"pos {pos}: layer output")
 
 
+def test_attention_layer_matches_oracle_past_one_batch(attn_setup):
+    """Positions whose chunks need more than one batch of S3 rows: a chunk is
+    ceil((pos + 1) / 16) positions, a batch 8 waves x 9 rows = 72, so from
+    position 1152 on the S3 loop reloads cache rows inside the loop. Up to the
+    last position a 4096-row cache allows. The layer output is bit-exact."""
+    S = attn_setup
+    w, rng = S["w"], S["rng"]
+    max_pos = 4096
+    cos, sin = rope.yarn_tables(max_pos)
+    cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    host_cache = orc.bf16_round(rng.standard_normal((max_pos, L + DR), dtype=np.float32))
+    cache_d = dev16(bits(host_cache))
+    dec = ops.AttnDecoder(DSV2_LITE)
+    for pos in (1151, 1152, 1153, 1300, 2047, 3000, max_pos - 1):
+        batches = -(-(-(-(pos + 1) // 16)) // 72)
+        say(f"attention pos {pos} ({batches} S3 batches)")
+        x = _x(rng)
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty_like(xd)
+        dec.attn_into(S["layer"], xd, yd, cache_d, pos, None, cos_d, sin_d)
+        torch.cuda.synchronize()
+        assert dec.status() == 0
+        g_row = orc.bf16_to_f32(cache_d[pos].cpu().numpy().view(np.uint16))
+        r = orc.attention(w, x, host_cache, pos, cos, sin)
+        np.testing.assert_array_equal(g_row.view(np.uint32), r["row"].view(np.uint32),
+                                      err_msg=f"pos {pos}: cache row")
+        host_cache[pos] = g_row
+        want = orc.bf16_round(x + r["out"])
+        got = yd.cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32),
+                                      err_msg=f"pos {pos}: layer output")
+
+
 def test_attention_in_place_and_device_position_and_graph(attn_setup):
     """x_out may alias x; a device position gives the same bits as the host
     position; a captured graph replays at the positions the device holds."""

@@ -136,6 +136,35 @@ def test_fused_step_equals_separate_launches_on_deep_tables(model, n_layers):
     say(f"picks {p1.tolist()}")
 
 
+def test_fused_step_equals_separate_launches_at_long_positions(model):
+    """Steps from position 2300 over a seeded cache, where every attention
+    chunk needs several batches of S3 rows: one launch per step equals the
+    separate launches bit for bit."""
+    blob, lay = model
+    g = torch.Generator(device="cuda").manual_seed(12)
+    prompt = torch.from_numpy(
+        np.random.default_rng(8).integers(0, lay_mod.VOCAB, 4).astype(np.int32)).cuda()
+    outs = []
+    for fused in (False, True):
+        dec = ops.Decoder(blob, lay, DSV2_LITE, max_pos=2400, fused=fused)
+        dec.cache.copy_((0.5 * torch.randn(dec.cache.shape, generator=g.manual_seed(12),
+                                           device="cuda")).to(torch.bfloat16).view(torch.int16))
+        dec.reset(2300)
+        xs, picks = [], []
+        for p in range(4):
+            dec.token.copy_(prompt[p:p + 1])
+            dec.enqueue_step()
+            xs.append(dec.x.clone())
+            picks.append(dec.token_out.clone())
+        torch.cuda.synchronize()
+        assert dec.status() == 0
+        outs.append((torch.stack(xs).view(torch.int32).cpu(), torch.cat(picks).cpu(),
+                     dec.cache[:, 2300:2304].cpu()))
+    say(f"fused at 2300..2303 equal: {[torch.equal(a, b) for a, b in zip(*outs)]}")
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_fused_step_rejects_a_bad_position_without_running(model):
     """A device position outside [0, max_pos) raises FLEET_MOE_ABORT_POSITION
     and the step does nothing (the cache and the position are untouched)."""
