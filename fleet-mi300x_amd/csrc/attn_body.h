@@ -376,11 +376,28 @@ __device__ __forceinline__ bool tagged(const u32x4& v, uint32_t tag) {
 // runs out (or finds the sticky status set by another wait) raises
 // FLEET_MOE_ABORT_ATTN_WAIT and returns false; the caller carries on with
 // whatever was read, so the grid always drains.
-
+// kOne: one poll in flight per wave (the layer's own launch: 21.0 -> 20.0 us
+// against two); otherwise two, half a round trip apart (the whole-step
+// kernel, where one in flight measured 0.2-0.5 us slower per layer).
+template <bool kOne>
 __device__ bool poll16(const void* base, int off, bool active, uint32_t tag, u32x4& v,
                        Workspace* ws) {
     const __amdgpu_buffer_rsrc_t r = rsrc(base);
     const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (kOne) {
+        // one poll in flight, a short sleep between rounds
+        u32x4 a = active ? ld_dev16(r, off) : z;
+        for (uint32_t it = 0;; ++it) {
+            if (__all(!active || tagged(a, tag))) { v = a; return true; }
+            __builtin_amdgcn_s_sleep(1);
+            a = active ? ld_dev16(r, off) : z;
+            if (it >= kSpinLimit || ((it & 1023) == 1023 && ld_agent(&ws->abort) != 0)) {
+                if ((fm_tid() & (kLanes - 1)) == 0) raise(ws, FLEET_MOE_ABORT_ATTN_WAIT);
+                v = a;
+                return false;
+            }
+        }
+    }
     // two polls in flight, half a round trip apart
     u32x4 a = active ? ld_dev16(r, off) : z;
     __builtin_amdgcn_s_sleep(8);
@@ -664,7 +681,7 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
     // ---- S2: q_c[h][32k .. 32k+31] = sum over the 128 rows of W_UK q_nope
     {
         u32x4 qn;
-        poll16(ws->qkv_t, 4 * (h * (kNope + kRope) + kUkRows * wave) + 16 * lane, lane < 4,
+        poll16<!kMega>(ws->qkv_t, 4 * (h * (kNope + kRope) + kUkRows * wave) + 16 * lane, lane < 4,
                tag, qn, ws);
         ATTN_TRACE(4);
         // lane needs q_nope[16 wave + lane / 4]: word (lane / 4) % 4 of lane lane / 16
@@ -726,12 +743,12 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
         u32x4 v;
         if (wave < 4) {
             // q_c of head h: 512 tagged words, 2 per lane
-            poll16(ws->qc_t, 8 * (h3 * kLora + 128 * wave + 2 * lane), true, tag, v, ws);
+            poll16<!kMega>(ws->qc_t, 8 * (h3 * kLora + 128 * wave + 2 * lane), true, tag, v, ws);
             L.u.s3.qc[128 * wave + 2 * lane] = tagged_f32(v.x, v.y);
             L.u.s3.qc[128 * wave + 2 * lane + 1] = tagged_f32(v.z, v.w);
         } else if (wave == 4) {
             // q_pe of head h before RoPE: 64 words, 4 per lane
-            poll16(ws->qkv_t, 4 * (h3 * (kNope + kRope) + kNope) + 16 * lane, lane < 16,
+            poll16<!kMega>(ws->qkv_t, 4 * (h3 * (kNope + kRope) + kNope) + 16 * lane, lane < 16,
                    tag, v, ws);
             if (lane < 16) {
                 L.u.s3.qpe_raw[4 * lane] = __uint_as_float(v.x << 16);
@@ -743,7 +760,7 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
             // kv_a (576 words): waves 5, 6, 7 take words 0..255, 256..511, 512..575
             const int w0 = 256 * (wave - 5);
             const bool act = w0 + 4 * lane < kLora + kRope;
-            poll16(ws->qkv_t, 4 * (kQDim + w0) + 16 * lane, act, tag, v, ws);
+            poll16<!kMega>(ws->qkv_t, 4 * (kQDim + w0) + 16 * lane, act, tag, v, ws);
             if (act) {
                 L.u.s3.kva[w0 + 4 * lane] = __uint_as_float(v.x << 16);
                 L.u.s3.kva[w0 + 4 * lane + 1] = __uint_as_float(v.y << 16);
@@ -903,11 +920,11 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
         // wave w: chunks 2w and 2w + 1 (column 32k + lane % 32), and their max / sum
         const int c = 2 * wave + (lane >> 5);
         u32x4 v;
-        poll16(ws->o_t, (int)(((h * kChunks + c) * kLora + kQcCols * k + (lane & 31)) * 16),
+        poll16<!kMega>(ws->o_t, (int)(((h * kChunks + c) * kLora + kQcCols * k + (lane & 31)) * 16),
                c < n_used, tag, v, ws);
         if (c < n_used) L.u.s4.mo[c][lane & 31] = tagged_f64(v);
         const int cm = 2 * wave + (lane >> 1);
-        poll16(ws->ml_t, (int)(((h * kChunks + cm) * 8 + 4 * (lane & 1)) * 4),
+        poll16<!kMega>(ws->ml_t, (int)(((h * kChunks + cm) * 8 + 4 * (lane & 1)) * 4),
                lane < 4 && cm < n_used, tag, v, ws);
         if (lane < 4 && cm < n_used) {
             if (lane & 1) L.u.s4.ml[cm] = tagged_f64(v);
@@ -931,7 +948,7 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
         }
         ATTN_TRACE(11);
         // o_c of head h, columns 64 wave .. 64 wave + 63 (two per lane)
-        poll16(ws->oc_t, 8 * (h * kLora + 64 * wave + 2 * lane), lane < 32, tag, v, ws);
+        poll16<!kMega>(ws->oc_t, 8 * (h * kLora + 64 * wave + 2 * lane), lane < 32, tag, v, ws);
         ATTN_TRACE(12);
         if (lane < 32) {
             L.u.s4.oc[64 * wave + 2 * lane] = tagged_f32(v.x, v.y);
@@ -961,7 +978,7 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
     // ---- S5: o_proj rows 8 wg .. 8 wg + 7 and the residual add
     {
         u32x4 v;
-        poll16(ws->out_t[wg % kOutCopies], 4 * (256 * wave + 4 * lane), true, tag, v, ws);
+        poll16<!kMega>(ws->out_t[wg % kOutCopies], 4 * (256 * wave + 4 * lane), true, tag, v, ws);
         ATTN_TRACE(14);
         next();
         reinterpret_cast<uint2*>(L.u.s5.outv)[64 * wave + lane] =
