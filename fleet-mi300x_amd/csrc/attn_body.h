@@ -811,7 +811,7 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
         for (int jj = 0; jj < 8; ++jj) qd[jj] = (double)L.u.s3.qc[8 * lane + jj];
         const float qp = L.u.s3.qpe[lane];
         constexpr int kSum = 16;                           // kBatch rows reduced together
-        static_assert(kBatch <= kSum, "one reduction per batch");
+        static_assert(kBatch < kSum, "one reduction per batch, and a free value index");
         int ri = 0;                                        // the row whose score this lane gets
 #pragma unroll
         for (int k2 = 0; k2 < 4; ++k2)
@@ -838,8 +838,11 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
             const bool valid = ri < kBatch && base + kWaves * ri < t_end;
             const double sv = valid ? tot * P.scale : -INFINITY;
             const double m_new = fmax(m_w, wave_max64(sv));
-            const double fo = exp(m_w - m_new);            // 0 while nothing is accumulated
-            const double ev = exp(sv - m_new);             // 0 for rows that are not there
+            // one exponential per lane: the rows' exp(s - m_new) in the lanes
+            // that hold a row, the rescale exp(m_old - m_new) in the last lane
+            // (whose value index, 15, holds no row)
+            const double ev = exp(ri == kSum - 1 ? m_w - m_new : sv - m_new);
+            const double fo = readlane64(ev, kMsumLane16.lane[kSum - 1]);   // 0 while nothing is accumulated
             l_w *= fo;
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) o[jj] *= fo;
@@ -865,8 +868,9 @@ __device__ __forceinline__ void attn_layer(const Params& P, Lds& L, u32x4 (&pre)
             const float rk = __uint_as_float((uint32_t)L.u.s3.row[kLora + lane] << 16);
             const double sv = wave_sum64(dot8_xd(rc, qd, (double)(rk * qp))) * P.scale;
             const double m_new = fmax(m_w, sv);
-            const double fo = exp(m_w - m_new);
-            const double e = exp(sv - m_new);
+            const double ex = exp(lane == 0 ? m_w - m_new : sv - m_new);   // one per lane
+            const double fo = readlane64(ex, 0);
+            const double e = readlane64(ex, 1);
             const uint32_t cw[4] = {rc.x, rc.y, rc.z, rc.w};
             l_w = fma(l_w, fo, e);
 #pragma unroll
