@@ -188,7 +188,10 @@ constexpr int tree_depth(int n) { return n <= 1 ? 0 : 1 + tree_depth((n + 1) / 2
 // sums are added in a fixed order through v_readlane. Every lane returns the
 // same value and the order of additions never changes, so results are
 // bitwise reproducible.
-#define FLEET_DPP(v, ctrl) __builtin_amdgcn_update_dpp(0, (v), (ctrl), 0xF, 0xF, false)
+// Every control used (quad permutes, row mirrors, row rotates) gives each
+// lane a source inside its row, so no lane reads an "old" value: the move has
+// none (bound_ctrl), and no register has to be cleared before it.
+#define FLEET_DPP(v, ctrl) __builtin_amdgcn_mov_dpp((v), (ctrl), 0xF, 0xF, true)
 
 __device__ __forceinline__ float wave_sum(float v) {
     v += __int_as_float(FLEET_DPP(__float_as_int(v), 0xB1));   // quad_perm [1,0,3,2]
