@@ -19,6 +19,7 @@ torch = pytest.importorskip("torch")
 from fleet_moe import ops, synth  # noqa: E402
 from fleet_moe.layout import DSV2_LITE  # noqa: E402
 from oracle import moe_oracle as orc  # noqa: E402
+from oracle_batch import moe_layer_batched  # noqa: E402
 
 REL_TOL = 1e-2
 
@@ -30,24 +31,6 @@ def say(msg: str) -> None:
 def rel_err(got, want) -> float:
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
-
-
-def moe_layer_batched(pl, x) -> dict:
-    """orc.moe_layer over a batch of tokens [T, H], composed from the same
-    oracle functions: one routing call, the shared expert as one batch, each
-    routed expert once over the tokens that selected it (its exactly rounded
-    GEMVs do not depend on the batching), the combine in selection order."""
-    x = np.asarray(x, np.float32)
-    x_n = orc.rms_norm(x, pl.gamma_f32())
-    _, ids, ws = orc.route(pl.router_f32(), x_n)
-    shared = orc.mlp_unit(*pl.shared_f32(), x_n)
-    e_out = np.zeros(ids.shape + (x.shape[1],), np.float32)
-    for e in np.unique(ids):
-        t, k = np.nonzero(ids == e)
-        e_out[t, k] = orc.mlp_unit(*pl.expert_f32(int(e)), x_n[t])
-    terms = [orc.bf16_round(ws[:, k:k + 1] * e_out[:, k]) for k in range(ids.shape[1])]
-    out = orc.combine(terms, shared)
-    return {"ids": ids, "weights": ws, "out": out, "x_out": orc.bf16_round(x + out)}
 
 
 @pytest.fixture(scope="module")

@@ -437,6 +437,34 @@ def test_moe_layer_fp32_reference_arithmetic_agrees(full_layer):
         assert rel_err(r["x_out"], e["x_out"]) <= 1e-2
 
 
+def test_batched_moe_layer_equals_the_per_token_oracle(full_layer):
+    """tests/oracle_batch.py (the GPU tests' checker over many tokens) gives
+    the per-token oracle's ids, weights and layer outputs bit for bit; with
+    two slots' weights exchanged (a plausible batching slip) it does not."""
+    from oracle_batch import moe_layer_batched
+    _, _, pl = full_layer
+    rng = np.random.default_rng(15)
+    x = orc.bf16_round(rng.standard_normal((12, 2048)).astype(np.float32))
+    got = moe_layer_batched(pl, x)
+    for t in range(12):
+        e = orc.moe_layer(pl, x[t])
+        np.testing.assert_array_equal(got["ids"][t], e["ids"])
+        np.testing.assert_array_equal(got["weights"][t].view(np.uint32), e["weights"].view(np.uint32))
+        np.testing.assert_array_equal(got["x_out"][t].view(np.uint32), e["x_out"].view(np.uint32))
+    # planted mistake: slots 0 and 1 take each other's weights
+    real = orc.route
+
+    def swapped(*a, **k):
+        logits, ids, ws = real(*a, **k)
+        return logits, ids, ws[..., [1, 0, 2, 3, 4, 5]]
+    try:
+        orc.route = swapped
+        bad = moe_layer_batched(pl, x)
+    finally:
+        orc.route = real
+    assert not np.array_equal(bad["x_out"].view(np.uint32), got["x_out"].view(np.uint32))
+
+
 def test_moe_grouped_equals_per_token_and_hf_rule():
     rng = np.random.default_rng(13)
     layer, _ = pack_tiny(rng, 64, 16, 8, 2, 0.08)
