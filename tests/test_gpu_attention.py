@@ -164,6 +164,43 @@ def test_attention_layer_matches_oracle_past_one_batch(attn_setup):
                                       err_msg=f"pos {pos}: layer output")
 
 
+def test_attention_layer_matches_oracle_at_64_positions(attn_setup):
+    """64 positions over a 4096-row cache, in a seeded random order (8 of them
+    at the chunking's edges: the first positions, where chunks hold one row and
+    some hold none, a last chunk of one row, one and several S3 batches): cache
+    row and layer output bit-exact at each, every call seeing the rows the
+    calls before it wrote."""
+    S = attn_setup
+    w = S["w"]
+    rng = np.random.default_rng(23)
+    max_pos = 4096
+    cos, sin = rope.yarn_tables(max_pos)
+    cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    host_cache = orc.bf16_round(rng.standard_normal((max_pos, L + DR), dtype=np.float32))
+    cache_d = dev16(bits(host_cache))
+    dec = ops.AttnDecoder(DSV2_LITE)
+    edges = [0, 14, 15, 16, 255, 1151, 2048, max_pos - 1]
+    rest = rng.choice(np.setdiff1d(np.arange(max_pos), edges), 56, replace=False)
+    order = rng.permutation(np.concatenate([edges, rest]))
+    for i, pos in enumerate(order.tolist()):
+        if i % 16 == 0:
+            say(f"attention, positions {i}..{i + 15} of 64")
+        x = _x(rng)
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty_like(xd)
+        dec.attn_into(S["layer"], xd, yd, cache_d, pos, None, cos_d, sin_d)
+        torch.cuda.synchronize()
+        g_row = orc.bf16_to_f32(cache_d[pos].cpu().numpy().view(np.uint16))
+        r = orc.attention(w, x, host_cache, pos, cos, sin)
+        np.testing.assert_array_equal(g_row.view(np.uint32), r["row"].view(np.uint32),
+                                      err_msg=f"pos {pos}: cache row")
+        host_cache[pos] = g_row
+        want = orc.bf16_round(x + r["out"])
+        np.testing.assert_array_equal(yd.cpu().numpy().view(np.uint32), want.view(np.uint32),
+                                      err_msg=f"pos {pos}: layer output")
+    assert dec.status() == 0
+
+
 def test_attention_in_place_and_device_position_and_graph(attn_setup):
     """x_out may alias x; a device position gives the same bits as the host
     position; a captured graph replays at the positions the device holds."""
