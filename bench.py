@@ -126,6 +126,7 @@ def counter_view(result: dict, profiled: dict) -> dict:
         "dense": dense,
         "moe_layer_in_column": (col - dense) / 26 if col and dense else None,
         "column": col,
+        "decode_step": (get("full_decode", "ms_per_token") or 0) * 1e3 or None,
     }
     for t in ("T4", "T16", "T64"):
         times[f"grouped_{t}"] = get("grouped", t, "us_per_step")

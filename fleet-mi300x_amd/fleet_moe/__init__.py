@@ -5,7 +5,9 @@ Python host side over the C ABI of libfleet_moe.so (include/fleet_moe.h):
 checkpoint into that layout), `synth` / `synth_gpu` (seeded synthetic weights
 on the host / device), `rope` (the YaRN rotary tables), `ops` (device buffers
 and calls), `descriptors` (the reference's 64-byte task descriptors: the MoE
-task kinds planned onto library calls).
+task kinds planned onto library calls). Diagnostics, run as modules:
+`stage_trace` (stage timelines from the stamped build) and `step_run` (a short
+run of the one-launch decode step for counter passes).
 """
 from .layout import DSV2_LITE, MoeDims  # noqa: F401
 
